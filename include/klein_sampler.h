@@ -1,0 +1,108 @@
+/* klein_sampler.h — C ABI of the MI355X (gfx950) token sampler.
+ *
+ * Drop-in for klein's sampling path: klein::Sampler (src/sampler.h:25-38, src/sampler.cpp:11-89) and the MTP
+ * verify accept loop of Engine::generate (src/engine.cpp:563-575). Plain C types and pointers only; every entry
+ * point returns a status (KLS_OK = 0) and never throws. The C++ class klein::Sampler in klein_amd/csrc/sampler.h
+ * keeps the reference's interface on top of these functions.
+ *
+ * Results equal the reference sampler's on the same logits and the same uniform draws: token ids, top-k id sets
+ * and accepted-draft counts bit for bit (on equal values the lower id wins), probabilities to the bit as well.
+ * The uniform `u` of a draw is the value std::uniform_real_distribution<double> would derive from the sampler's
+ * mt19937_64 (libstdc++ generate_canonical: double(x) / 2^64, clamped below 1); the caller supplies it.
+ */
+#ifndef KLEIN_SAMPLER_H_
+#define KLEIN_SAMPLER_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum kls_status {
+    KLS_OK = 0,
+    KLS_ERR_INVALID_ARG = 1, /* null pointer, n_vocab <= 0, n_vocab differing from the handle's, nb < 1 */
+    KLS_ERR_RANGE = 2,       /* rows above the handle's capacity, a token id outside [0, n_vocab) */
+    KLS_ERR_UNSUPPORTED = 3, /* a parameter combination this build does not implement */
+    KLS_ERR_HIP = 4,         /* a HIP runtime call failed (the message names it: kls_last_error) */
+    KLS_ERR_NO_DEVICE = 5,   /* no GPU visible */
+    KLS_ERR_OOM = 6          /* device or pinned allocation failed */
+};
+
+/* klein::SamplerParams (src/sampler.h:13-22): same fields, order and defaults (temperature 1, top_k 20,
+ * top_p 0.95, min_p 0, presence 0, frequency 0, repetition 1, seed 0). temperature <= 0 selects greedy;
+ * top_k <= 0 or >= n_vocab means no limit. The seed is used by the C++ wrapper's mt19937_64 only. */
+typedef struct kls_params {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float min_p;
+    float presence_penalty;
+    float frequency_penalty;
+    float repetition_penalty;
+    uint64_t seed;
+} kls_params;
+
+typedef struct kls_sampler* kls_handle;
+
+/* hipStream_t, passed as a plain pointer; NULL selects the handle's own stream. */
+typedef void* kls_stream;
+
+/* Replaces Sampler::Sampler (src/sampler.cpp:11). Binds the current HIP device, allocates every buffer the
+ * handle will use (no allocation happens in the calls below), and starts with an empty token history.
+ * max_rows bounds the rows of kls_verify and kls_sample_batch. */
+int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* out);
+
+int kls_destroy(kls_handle h);
+
+/* Replaces Sampler::reset (src/sampler.cpp:13): clears the token history. */
+int kls_reset(kls_handle h);
+
+/* Replaces Sampler::accept (src/sampler.cpp:15): counts one more occurrence of `token` for the penalties. */
+int kls_accept(kls_handle h, int32_t token);
+
+/* Replaces Sampler::sample (src/sampler.cpp:17-89) for one row of n_vocab f32 logits. `logits` may be a device
+ * pointer (read in place) or a host pointer (copied to the device first). `u` is the draw's uniform (ignored
+ * when temperature <= 0). Penalties use the history given through kls_accept. Synchronous. */
+int kls_sample(kls_handle h, const float* logits, int n_vocab, double u, int32_t* out_token);
+
+/* Replaces the verify/accept loop of Engine::generate (src/engine.cpp:563-575). `logits` holds nb rows of
+ * n_vocab f32 (row i at logits + i*n_vocab; device or host pointer); row 0 is the main position and rows
+ * 1..nb-1 the draft positions. drafts[i] (i < nb-1) is the draft token batch[i+1]; u[i] the uniform of row i.
+ * Row i is sampled with the history after accepting t_0..t_{i-1}; drafts are accepted while drafts[i] == t_i.
+ * On return out_tokens[0..*out_accepted] are the emitted tokens (later entries are unspecified) and the
+ * emitted tokens have been added to the history, as the engine's accept(t) calls do (engine.cpp:567).
+ * The caller-side stops of the engine (end-of-generation token, n_predict, callback) stay with the caller.
+ * The step runs as one hipGraph launch on `stream`; host-side inputs and outputs go through pinned memory. */
+int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
+               int32_t* out_tokens, int32_t* out_accepted, kls_stream stream);
+
+/* Batched sampling of n_rows independent rows, all on the device, asynchronous on `stream` (no host sync).
+ * Row r is at d_logits + r*row_stride floats; its token history is d_hist_ids[d_hist_off[r] .. d_hist_off[r+1])
+ * (raw ids, repeats counted; d_hist_off has n_rows+1 entries; NULL offsets = no history). d_u[r] is row r's
+ * uniform. Tokens are written to d_out_tokens[r]. The handle's own history is not used or changed. Each row
+ * equals one Sampler::sample call on that row after accept() of its history ids. */
+int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_hist_off,
+                     const int32_t* d_hist_ids, const double* d_u, int32_t* d_out_tokens, kls_stream stream);
+
+/* The sorted top-k candidates of `row` from the last completed call (kls_sample: row 0): ids, softmax
+ * probabilities before min-p/top-p truncation (up to `cap`), k, and how many survived min-p/top-p.
+ * Synchronizes the handle's stream. For tests and tooling; not needed on the sampling path. */
+int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int cap, int32_t* n_k, int32_t* n_kept);
+
+/* Test hook, no counterpart in the reference: writes the sampler's expf of the n consecutive float bit
+ * patterns lo, lo+1, ... to device memory `d_out`, asynchronously on `stream`, so tests can compare the device
+ * exponential with the host libm's std::exp(float) (src/sampler.cpp:57) over whole ranges of inputs. */
+int kls_debug_expf(uint32_t lo, long long n, float* d_out, kls_stream stream);
+
+/* Human-readable name of a status code. */
+const char* kls_status_string(int status);
+
+/* Thread-local text of the last failure on this thread (empty when none). */
+const char* kls_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KLEIN_SAMPLER_H_ */

@@ -1,0 +1,492 @@
+// C-ABI layer of the gfx950 token sampler (include/klein_sampler.h).
+//
+// A handle replaces one klein::Sampler (src/sampler.h:25-38): it holds the parameters, the token history
+// (src/sampler.h:36, counts_), and every device / pinned buffer its calls use, all allocated in kls_create.
+// The history lives on the host as the reference keeps it (id -> count) and on the device as a list of
+// unique ids with counts, bucketed by id range; ids accepted since the last upload travel with each call in
+// pinned memory and are counted on the device on top of the uploaded list, so an engine step uploads nothing.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "klein_sampler.h"
+#include "kls_internal.h"
+
+using namespace kls;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int status, const char* what, hipError_t e = hipSuccess) {
+    char buf[256];
+    if (e != hipSuccess)
+        snprintf(buf, sizeof buf, "%s: %s", what, hipGetErrorString(e));
+    else
+        snprintf(buf, sizeof buf, "%s", what);
+    g_err = buf;
+    return status;
+}
+
+#define KLS_HIP(expr)                                                        \
+    do {                                                                     \
+        hipError_t e_ = (expr);                                              \
+        if (e_ != hipSuccess) return fail(KLS_ERR_HIP, #expr, e_);           \
+    } while (0)
+
+constexpr int BATCH_HISTORY_PER_ROW = 65536;  // raw history ids per row the batch entry point can take
+
+}  // namespace
+
+struct kls_sampler {
+    kls_params p{};
+    SamplingParams sp{};
+    bool greedy = false, penalize = false;
+    int k = 0;
+    int V = 0, max_rows = 0, device = 0;
+    int bucket_shift = MIN_BUCKET_SHIFT, n_buckets = 0;
+    int seg_len_override = 0, target_wg = 256;
+    hipStream_t stream = nullptr;
+
+    // token history: host copy (as the reference's counts_) + what has reached the device
+    std::unordered_map<int32_t, int32_t> counts;
+    std::vector<int32_t> pending;  // accepted since the last upload, in order
+    int32_t* d_hist_ids = nullptr;  // [V] unique ids, bucketed
+    int32_t* d_hist_w = nullptr;    // [V] counts
+    int32_t* d_hist_boff = nullptr; // [n_buckets + 1]
+    int32_t* h_stage = nullptr;     // pinned staging for uploads: 2*V + n_buckets + 1
+
+    // batch history partition
+    int32_t* d_part_ids = nullptr;  // [max_rows * BATCH_HISTORY_PER_ROW]
+    int32_t* d_part_boff = nullptr; // [max_rows][n_buckets + 1]
+    int part_cap = 0;
+
+    // scratch
+    uint64_t* d_seg_cand = nullptr;
+    uint32_t* d_row_ticket = nullptr;
+    uint64_t* d_row_thr = nullptr;
+    uint32_t* d_step_ticket = nullptr;
+    int32_t* d_tokens = nullptr;
+    int32_t* d_accepted = nullptr;
+    uint64_t* d_dbg_keys = nullptr;
+    float* d_dbg_probs = nullptr;
+    int32_t* d_dbg_meta = nullptr;
+    float* d_rows_buf = nullptr;  // host logits are copied here
+    int max_segs = 0;
+
+    // pinned host blocks
+    CallBlock* call = nullptr;    // host view
+    ResultBlock* res = nullptr;
+    CallBlock* call_dev = nullptr;  // device views of the same mapped memory
+    ResultBlock* res_dev = nullptr;
+    uint32_t seq = 0;
+
+    // verify graph, keyed by what it bakes in
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    const float* g_logits = nullptr;
+    int g_rows = 0;
+    bool g_valid = false;
+};
+
+namespace {
+
+bool is_device_ptr(const void* p) {
+    hipPointerAttribute_t attr;
+    const hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void) hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+void segments_for(const kls_sampler* h, int rows, bool penalize, int* seg_len, int* segs) {
+    const int bw = 1 << h->bucket_shift;
+    long long sl = h->seg_len_override;
+    if (sl <= 0) {
+        const long long per = ((long long) h->V * rows + h->target_wg - 1) / h->target_wg;
+        sl = per;
+    }
+    sl = ((sl + bw - 1) / bw) * bw;
+    sl = std::max<long long>(sl, bw);
+    if (penalize) sl = std::min<long long>(sl, SEG_MAX_PENALIZED);
+    sl = std::min<long long>(sl, ((long long) h->V + bw - 1) / bw * bw);
+    *seg_len = (int) sl;
+    *segs = (int) ((h->V + sl - 1) / sl);
+}
+
+// Rebuilds the device history from the host counts (bucketed unique ids + counts) and clears `pending`.
+int upload_history(kls_sampler* h, hipStream_t s) {
+    std::vector<std::pair<int32_t, int32_t>> ent(h->counts.begin(), h->counts.end());
+    std::sort(ent.begin(), ent.end());
+    int32_t* ids = h->h_stage;
+    int32_t* w = h->h_stage + h->V;
+    int32_t* bo = h->h_stage + 2 * (size_t) h->V;
+    const int n = (int) ent.size();
+    int b = 0;
+    for (int i = 0; i < n; ++i) {
+        ids[i] = ent[i].first;
+        w[i] = ent[i].second;
+        const int bi = ent[i].first >> h->bucket_shift;
+        while (b <= bi) bo[b++] = i;
+    }
+    while (b <= h->n_buckets) bo[b++] = n;
+    // the copies read the pinned staging asynchronously: wait for them before the staging is reused
+    if (n > 0) {
+        KLS_HIP(hipMemcpyAsync(h->d_hist_ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
+        KLS_HIP(hipMemcpyAsync(h->d_hist_w, w, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
+    }
+    KLS_HIP(hipMemcpyAsync(h->d_hist_boff, bo, sizeof(int32_t) * (h->n_buckets + 1), hipMemcpyHostToDevice, s));
+    KLS_HIP(hipStreamSynchronize(s));
+    h->pending.clear();
+    return KLS_OK;
+}
+
+RowsArgs base_args(kls_sampler* h, const float* logits, int rows, int64_t stride) {
+    RowsArgs a{};
+    a.logits = logits;
+    a.row_stride = stride;
+    a.V = h->V;
+    a.n_rows = rows;
+    segments_for(h, rows, h->penalize, &a.seg_len, &a.segs);
+    a.p = h->sp;
+    a.bucket_shift = h->bucket_shift;
+    a.n_buckets = h->n_buckets;
+    a.seg_cand = h->d_seg_cand;
+    a.row_ticket = h->d_row_ticket;
+    a.row_thr = h->d_row_thr;
+    a.step_ticket = h->d_step_ticket;
+    a.out_tokens = h->d_tokens;
+    a.dbg_keys = h->d_dbg_keys;
+    a.dbg_probs = h->d_dbg_probs;
+    a.dbg_meta = h->d_dbg_meta;
+    return a;
+}
+
+// Arguments of a step over the handle's own history: rows read their uniforms and drafts from the pinned call
+// block, and count the handle's pending ids (and, for row i, drafts 0..i-1) on top of the uploaded history.
+RowsArgs step_args(kls_sampler* h, const float* logits, int rows, bool verify) {
+    RowsArgs a = base_args(h, logits, rows, h->V);
+    if (h->penalize) {
+        a.hist_ids = h->d_hist_ids;
+        a.hist_w = h->d_hist_w;
+        a.hist_boff = h->d_hist_boff;
+        a.hist_cap = h->V;
+        a.hist_shared = 1;
+        a.extra_a = h->call_dev->pending;
+        a.extra_a_n = &h->call_dev->n_pending;
+        a.extra_b = verify ? h->call_dev->drafts : nullptr;
+        a.extra_b_step = verify ? 1 : 0;
+    }
+    a.u = h->call_dev->u;
+    a.drafts = verify ? h->call_dev->drafts : nullptr;
+    a.out_accepted = h->d_accepted;
+    a.host_res = h->res_dev;
+    a.call = h->call_dev;
+    return a;
+}
+
+int check_handle(kls_handle h) {
+    if (!h) return fail(KLS_ERR_INVALID_ARG, "null handle");
+    return KLS_OK;
+}
+
+// Brings the device history up to date before a step: pending ids ride in the call block up to its capacity.
+int prepare_history(kls_sampler* h, hipStream_t s) {
+    if (!h->penalize) return KLS_OK;
+    if ((int) h->pending.size() > PENDING_CAP) {
+        const int st = upload_history(h, s);
+        if (st) return st;
+    }
+    h->call->n_pending = (int32_t) h->pending.size();
+    std::copy(h->pending.begin(), h->pending.end(), h->call->pending);
+    return KLS_OK;
+}
+
+// Launches one step over `rows` rows of the handle's history and waits for the results in the pinned block.
+int run_step(kls_sampler* h, const float* logits, int rows, bool verify, hipStream_t s) {
+    const float* dl = logits;
+    if (!is_device_ptr(logits)) {
+        KLS_HIP(hipMemcpyAsync(h->d_rows_buf, logits, sizeof(float) * (size_t) rows * h->V, hipMemcpyHostToDevice, s));
+        dl = h->d_rows_buf;
+    }
+    int st = prepare_history(h, s);
+    if (st) return st;
+    h->call->seq = ++h->seq;
+    h->res->seq = 0;
+    const RowsArgs a = step_args(h, dl, rows, verify);
+    if (verify) {
+        if (!h->g_valid || h->g_logits != dl || h->g_rows != rows) {
+            if (h->gexec) hipGraphExecDestroy(h->gexec);
+            if (h->graph) hipGraphDestroy(h->graph);
+            h->gexec = nullptr;
+            h->graph = nullptr;
+            h->g_valid = false;
+            KLS_HIP(hipStreamBeginCapture(h->stream, hipStreamCaptureModeRelaxed));
+            const hipError_t le = launch_rows(a, h->greedy, h->penalize, h->stream);
+            hipGraph_t g = nullptr;
+            const hipError_t ce = hipStreamEndCapture(h->stream, &g);
+            if (le != hipSuccess) return fail(KLS_ERR_HIP, "launch_rows (capture)", le);
+            if (ce != hipSuccess) return fail(KLS_ERR_HIP, "hipStreamEndCapture", ce);
+            h->graph = g;
+            KLS_HIP(hipGraphInstantiate(&h->gexec, h->graph, nullptr, nullptr, 0));
+            h->g_logits = dl;
+            h->g_rows = rows;
+            h->g_valid = true;
+        }
+        KLS_HIP(hipGraphLaunch(h->gexec, s));
+    } else {
+        KLS_HIP(launch_rows(a, h->greedy, h->penalize, s));
+    }
+    KLS_HIP(hipStreamSynchronize(s));
+    if (h->res->seq != h->call->seq) return fail(KLS_ERR_HIP, "step result not published");
+    return KLS_OK;
+}
+
+void add_history(kls_sampler* h, int32_t t) {
+    h->counts[t]++;
+    h->pending.push_back(t);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kls_status_string(int status) {
+    switch (status) {
+        case KLS_OK: return "ok";
+        case KLS_ERR_INVALID_ARG: return "invalid argument";
+        case KLS_ERR_RANGE: return "out of range";
+        case KLS_ERR_UNSUPPORTED: return "unsupported";
+        case KLS_ERR_HIP: return "HIP runtime error";
+        case KLS_ERR_NO_DEVICE: return "no GPU device";
+        case KLS_ERR_OOM: return "out of memory";
+        default: return "unknown status";
+    }
+}
+
+const char* kls_last_error(void) { return g_err.c_str(); }
+
+int kls_destroy(kls_handle h) {
+    if (!h) return fail(KLS_ERR_INVALID_ARG, "null handle");
+    (void) hipSetDevice(h->device);
+    if (h->stream) (void) hipStreamSynchronize(h->stream);
+    if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
+    if (h->graph) (void) hipGraphDestroy(h->graph);
+    void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_part_ids, h->d_part_boff, h->d_seg_cand,
+                   h->d_row_ticket, h->d_row_thr, h->d_step_ticket, h->d_tokens, h->d_accepted, h->d_dbg_keys,
+                   h->d_dbg_probs, h->d_dbg_meta, h->d_rows_buf};
+    for (void* p : dev)
+        if (p) (void) hipFree(p);
+    if (h->h_stage) (void) hipHostFree(h->h_stage);
+    if (h->call) (void) hipHostFree(h->call);
+    if (h->res) (void) hipHostFree(h->res);
+    if (h->stream) (void) hipStreamDestroy(h->stream);
+    delete h;
+    return KLS_OK;
+}
+
+int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* out) {
+    if (!params || !out) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    *out = nullptr;
+    if (n_vocab <= 0) return fail(KLS_ERR_INVALID_ARG, "n_vocab must be positive");
+    if (max_rows < 1) return fail(KLS_ERR_INVALID_ARG, "max_rows must be positive");
+    const int k = (params->top_k > 0 && params->top_k < n_vocab) ? params->top_k : n_vocab;
+    if (params->temperature > 0.0f && k > KCAP)
+        return fail(KLS_ERR_UNSUPPORTED, "top-k above 64 (including no limit) is not implemented");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+        (void) hipGetLastError();
+        return fail(KLS_ERR_NO_DEVICE, "no GPU visible");
+    }
+    kls_sampler* h = new kls_sampler();
+    h->p = *params;
+    h->V = n_vocab;
+    h->max_rows = max_rows;
+    h->k = k;
+    h->greedy = params->temperature <= 0.0f;
+    h->penalize = params->presence_penalty != 0.0f || params->frequency_penalty != 0.0f ||
+                  params->repetition_penalty != 1.0f;
+    h->sp = SamplingParams{params->temperature, params->top_p, params->min_p, params->presence_penalty,
+                           params->frequency_penalty, params->repetition_penalty, std::min(k, KCAP)};
+    while (((n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift) > MAX_BUCKETS) h->bucket_shift++;
+    h->n_buckets = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;
+    if (const char* e = getenv("KLS_SEG_LEN")) h->seg_len_override = atoi(e);
+    if (const char* e = getenv("KLS_TARGET_WG")) h->target_wg = std::max(1, atoi(e));
+    (void) hipGetDevice(&h->device);
+
+    auto oom = [&](const char* what, hipError_t e) {
+        kls_destroy(h);
+        return fail(KLS_ERR_OOM, what, e);
+    };
+    hipError_t e;
+    if ((e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking)) != hipSuccess) return oom("stream", e);
+    h->max_segs = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;  // smallest segment = one bucket
+    const size_t R = (size_t) max_rows;
+    h->part_cap = (int) std::min<size_t>(R * BATCH_HISTORY_PER_ROW, 1u << 30);
+#define ALLOC(ptr, bytes) \
+    if ((e = hipMalloc((void**) &(ptr), (bytes))) != hipSuccess) return oom(#ptr, e)
+    ALLOC(h->d_hist_ids, sizeof(int32_t) * n_vocab);
+    ALLOC(h->d_hist_w, sizeof(int32_t) * n_vocab);
+    ALLOC(h->d_hist_boff, sizeof(int32_t) * (h->n_buckets + 1));
+    ALLOC(h->d_part_ids, sizeof(int32_t) * (size_t) h->part_cap);
+    ALLOC(h->d_part_boff, sizeof(int32_t) * R * (h->n_buckets + 1));
+    ALLOC(h->d_seg_cand, sizeof(uint64_t) * R * h->max_segs * KCAP);
+    ALLOC(h->d_row_ticket, sizeof(uint32_t) * R);
+    ALLOC(h->d_row_thr, sizeof(uint64_t) * R);
+    ALLOC(h->d_step_ticket, sizeof(uint32_t));
+    ALLOC(h->d_tokens, sizeof(int32_t) * R);
+    ALLOC(h->d_accepted, sizeof(int32_t));
+    ALLOC(h->d_dbg_keys, sizeof(uint64_t) * R * KCAP);
+    ALLOC(h->d_dbg_probs, sizeof(float) * R * KCAP);
+    ALLOC(h->d_dbg_meta, sizeof(int32_t) * R * 2);
+    ALLOC(h->d_rows_buf, sizeof(float) * R * n_vocab);
+#undef ALLOC
+    if ((e = hipHostMalloc((void**) &h->h_stage, sizeof(int32_t) * (2 * (size_t) n_vocab + h->n_buckets + 1),
+                           hipHostMallocDefault)) != hipSuccess)
+        return oom("pinned staging", e);
+    if ((e = hipHostMalloc((void**) &h->call, sizeof(CallBlock), hipHostMallocMapped | hipHostMallocCoherent)) !=
+        hipSuccess)
+        return oom("pinned call block", e);
+    if ((e = hipHostMalloc((void**) &h->res, sizeof(ResultBlock), hipHostMallocMapped | hipHostMallocCoherent)) !=
+        hipSuccess)
+        return oom("pinned result block", e);
+    if ((e = hipHostGetDevicePointer((void**) &h->call_dev, h->call, 0)) != hipSuccess) return oom("mapped call", e);
+    if ((e = hipHostGetDevicePointer((void**) &h->res_dev, h->res, 0)) != hipSuccess) return oom("mapped res", e);
+    std::memset(h->call, 0, sizeof(CallBlock));
+    std::memset(h->res, 0, sizeof(ResultBlock));
+    // zero the self-resetting counters and bounds once; the kernels leave them zero after every launch
+    if ((e = hipMemsetAsync(h->d_row_ticket, 0, sizeof(uint32_t) * R, h->stream)) != hipSuccess) return oom("init", e);
+    if ((e = hipMemsetAsync(h->d_row_thr, 0, sizeof(uint64_t) * R, h->stream)) != hipSuccess) return oom("init", e);
+    if ((e = hipMemsetAsync(h->d_step_ticket, 0, sizeof(uint32_t), h->stream)) != hipSuccess) return oom("init", e);
+    if ((e = hipMemsetAsync(h->d_hist_boff, 0, sizeof(int32_t) * (h->n_buckets + 1), h->stream)) != hipSuccess)
+        return oom("init", e);
+    if ((e = hipStreamSynchronize(h->stream)) != hipSuccess) return oom("init", e);
+    *out = h;
+    return KLS_OK;
+}
+
+int kls_reset(kls_handle h) {
+    if (int st = check_handle(h)) return st;
+    h->counts.clear();
+    h->pending.clear();
+    (void) hipSetDevice(h->device);
+    return h->penalize ? upload_history(h, h->stream) : KLS_OK;
+}
+
+int kls_accept(kls_handle h, int32_t token) {
+    if (int st = check_handle(h)) return st;
+    if (token < 0 || token >= h->V) return fail(KLS_ERR_RANGE, "token outside [0, n_vocab)");
+    add_history(h, token);
+    return KLS_OK;
+}
+
+int kls_sample(kls_handle h, const float* logits, int n_vocab, double u, int32_t* out_token) {
+    if (int st = check_handle(h)) return st;
+    if (!logits || !out_token) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (n_vocab != h->V) return fail(KLS_ERR_INVALID_ARG, "n_vocab differs from the handle's");
+    (void) hipSetDevice(h->device);
+    h->call->u[0] = u;
+    const int st = run_step(h, logits, 1, false, h->stream);
+    if (st) return st;
+    *out_token = h->res->tokens[0];
+    return KLS_OK;
+}
+
+int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
+               int32_t* out_tokens, int32_t* out_accepted, kls_stream stream) {
+    if (int st = check_handle(h)) return st;
+    if (!logits || !u || !out_tokens || !out_accepted || (nb > 1 && !drafts))
+        return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (nb < 1) return fail(KLS_ERR_INVALID_ARG, "nb must be at least 1");
+    if (nb > h->max_rows || nb > VERIFY_MAX_ROWS) return fail(KLS_ERR_RANGE, "nb above the handle's capacity");
+    (void) hipSetDevice(h->device);
+    hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    for (int i = 0; i < nb; ++i) h->call->u[i] = u[i];
+    for (int i = 0; i + 1 < nb; ++i) h->call->drafts[i] = drafts[i];
+    const int st = run_step(h, logits, nb, true, s);
+    if (st) return st;
+    const int acc = h->res->accepted;
+    for (int i = 0; i <= acc; ++i) {
+        out_tokens[i] = h->res->tokens[i];
+        add_history(h, out_tokens[i]);
+    }
+    for (int i = acc + 1; i < nb; ++i) out_tokens[i] = h->res->tokens[i];
+    *out_accepted = acc;
+    return KLS_OK;
+}
+
+int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_hist_off,
+                     const int32_t* d_hist_ids, const double* d_u, int32_t* d_out_tokens, kls_stream stream) {
+    if (int st = check_handle(h)) return st;
+    if (!d_logits || !d_out_tokens || (!h->greedy && !d_u)) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if ((d_hist_off == nullptr) != (d_hist_ids == nullptr))
+        return fail(KLS_ERR_INVALID_ARG, "history offsets and ids go together");
+    if (n_rows < 1) return fail(KLS_ERR_INVALID_ARG, "n_rows must be positive");
+    if (n_rows > h->max_rows) return fail(KLS_ERR_RANGE, "n_rows above the handle's capacity");
+    if (row_stride < h->V) return fail(KLS_ERR_INVALID_ARG, "row_stride below n_vocab");
+    (void) hipSetDevice(h->device);
+    hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    RowsArgs a = base_args(h, d_logits, n_rows, row_stride);
+    const bool pen = h->penalize && d_hist_off != nullptr;
+    if (!pen) segments_for(h, n_rows, false, &a.seg_len, &a.segs);
+    if (pen) {
+        PartitionArgs pa{};
+        pa.hist_off = d_hist_off;
+        pa.hist_ids = d_hist_ids;
+        pa.n_rows = n_rows;
+        pa.V = h->V;
+        pa.bucket_shift = h->bucket_shift;
+        pa.n_buckets = h->n_buckets;
+        pa.cap = h->part_cap;
+        pa.part_ids = h->d_part_ids;
+        pa.boff = h->d_part_boff;
+        KLS_HIP(launch_partition(pa, s));
+        a.hist_ids = h->d_part_ids;
+        a.hist_boff = h->d_part_boff;
+        a.hist_cap = h->part_cap;
+        a.hist_shared = 0;
+    }
+    a.u = d_u;
+    a.out_tokens = d_out_tokens;
+    KLS_HIP(launch_rows(a, h->greedy, pen, s));
+    return KLS_OK;
+}
+
+int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int cap, int32_t* n_k, int32_t* n_kept) {
+    if (int st = check_handle(h)) return st;
+    if (row < 0 || row >= h->max_rows) return fail(KLS_ERR_RANGE, "row outside the handle's capacity");
+    if (cap < 0 || (cap > 0 && (!ids || !probs))) return fail(KLS_ERR_INVALID_ARG, "bad output buffers");
+    (void) hipSetDevice(h->device);
+    KLS_HIP(hipDeviceSynchronize());
+    uint64_t keys[KCAP];
+    float pr[KCAP];
+    int32_t meta[2];
+    KLS_HIP(hipMemcpy(keys, h->d_dbg_keys + (size_t) row * KCAP, sizeof keys, hipMemcpyDeviceToHost));
+    KLS_HIP(hipMemcpy(pr, h->d_dbg_probs + (size_t) row * KCAP, sizeof pr, hipMemcpyDeviceToHost));
+    KLS_HIP(hipMemcpy(meta, h->d_dbg_meta + (size_t) row * 2, sizeof meta, hipMemcpyDeviceToHost));
+    const int n = std::min(cap, std::min(meta[0], KCAP));
+    for (int i = 0; i < n; ++i) {
+        ids[i] = (int32_t) ~(uint32_t) keys[i];
+        probs[i] = pr[i];
+    }
+    if (n_k) *n_k = meta[0];
+    if (n_kept) *n_kept = meta[1];
+    return KLS_OK;
+}
+
+// Test hook: expf of the consecutive float bit patterns lo, lo+1, ... (n of them) into device memory `out`.
+int kls_debug_expf(uint32_t lo, long long n, float* out, kls_stream stream) {
+    if (!out || n < 0) return fail(KLS_ERR_INVALID_ARG, "bad arguments");
+    KLS_HIP(launch_expf_table(lo, n, out, (hipStream_t) stream));
+    return KLS_OK;
+}
+
+}  // extern "C"

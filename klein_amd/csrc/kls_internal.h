@@ -1,0 +1,109 @@
+// Internal interface between the C-ABI layer (kls_api.cpp) and the HIP kernels (kls_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kls {
+
+// Candidates kept per segment and per row on the fast path (one per lane of a wave64).
+constexpr int KCAP = 64;
+// Rows a verify step may carry (1 main + up to 15 drafts).
+constexpr int VERIFY_MAX_ROWS = 16;
+// History ids accepted since the last device upload that ride along with a call.
+constexpr int PENDING_CAP = 256;
+// Largest segment (vocabulary ids per workgroup) when penalties are on: its counts live in LDS (4 B per id).
+constexpr int SEG_MAX_PENALIZED = 8192;
+// History bucket width: history lists are partitioned into buckets of (1 << bucket_shift) ids, and segments
+// start on bucket boundaries so a workgroup finds its history slice with two loads.
+constexpr int MIN_BUCKET_SHIFT = 10;
+constexpr int MAX_BUCKETS = 1024;
+
+// Per-call inputs a graph-captured step reads from pinned host memory (written by the host before launch).
+struct CallBlock {
+    double u[VERIFY_MAX_ROWS];
+    int32_t drafts[VERIFY_MAX_ROWS];
+    int32_t n_pending;
+    uint32_t seq;
+    int32_t pending[PENDING_CAP];
+};
+
+// Results a step writes back to pinned host memory.
+struct ResultBlock {
+    int32_t tokens[VERIFY_MAX_ROWS];
+    int32_t accepted;
+    uint32_t seq;
+};
+
+struct SamplingParams {
+    float temperature;
+    float top_p;
+    float min_p;
+    float presence;
+    float frequency;
+    float repetition;
+    int32_t k;  // effective top-k (1..KCAP on the fast path)
+};
+
+struct RowsArgs {
+    const float* logits;
+    int64_t row_stride;  // floats between rows
+    int32_t V;
+    int32_t n_rows;
+    int32_t segs;
+    int32_t seg_len;  // multiple of the history bucket width
+    SamplingParams p;
+
+    // history: per row (or shared) bucketed id list with optional weights (counts); NULL hist_boff = none
+    const int32_t* hist_ids;
+    const int32_t* hist_w;     // NULL: every entry counts once
+    const int32_t* hist_boff;  // [rows or 1][n_buckets + 1] absolute offsets into hist_ids
+    int32_t hist_cap;          // entries of hist_ids that may be read
+    int32_t hist_shared;       // 1: all rows use the first bucket-offset row
+    int32_t bucket_shift;
+    int32_t n_buckets;
+    // extra history ids counted on top: list A (count read from memory) for every row, list B's first
+    // row*extra_b_step entries for row `row` (the verify step's drafts on the accepted path)
+    const int32_t* extra_a;
+    const int32_t* extra_a_n;
+    const int32_t* extra_b;
+    int32_t extra_b_step;
+
+    const double* u;  // [n_rows]
+
+    // scratch (self-resetting between launches)
+    uint64_t* seg_cand;     // [n_rows][segs][KCAP]
+    uint32_t* row_ticket;   // [n_rows]
+    uint64_t* row_thr;      // [n_rows]
+    uint32_t* step_ticket;  // [1]
+
+    // outputs
+    int32_t* out_tokens;    // [n_rows] device
+    uint64_t* dbg_keys;     // [n_rows][KCAP] final sorted candidate keys
+    float* dbg_probs;       // [n_rows][KCAP]
+    int32_t* dbg_meta;      // [n_rows][2]: k, kept
+    // verify step (NULL drafts: no accept computation)
+    const int32_t* drafts;  // [n_rows-1]
+    int32_t* out_accepted;  // device
+    ResultBlock* host_res;  // pinned, may be NULL
+    const CallBlock* call;  // for the sequence number, may be NULL
+};
+
+struct PartitionArgs {
+    const int32_t* hist_off;  // [n_rows + 1]
+    const int32_t* hist_ids;
+    int32_t n_rows;
+    int32_t V;
+    int32_t bucket_shift;
+    int32_t n_buckets;
+    int32_t cap;              // entries of part_ids (offsets are clamped to it)
+    int32_t* part_ids;        // same indexing as hist_ids
+    int32_t* boff;            // [n_rows][n_buckets + 1]
+};
+
+// Launchers (kls_kernels.hip). Return hipSuccess or the launch error.
+hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_t s);
+hipError_t launch_partition(const PartitionArgs& a, hipStream_t s);
+hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s);
+
+}  // namespace kls

@@ -1,0 +1,76 @@
+"""CPU checks of the C ABI library: it loads, exports every entry point include/klein_sampler.h declares, and
+reports argument errors before touching a GPU. No compute call is made here."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from klein_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    syms = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            syms |= set(re.findall(r"^\s*(?:int|const char\*)\s+(kls_\w+)\s*\(", text, re.M))
+    return syms
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    syms = declared_symbols()
+    assert syms and syms == set(_lib.EXPORTS)
+    for s in syms:
+        assert hasattr(L, s), s
+
+
+def test_status_strings():
+    assert _lib.status_string(0) == "ok"
+    assert _lib.status_string(_lib.KLS_ERR_RANGE) == "out of range"
+    assert _lib.status_string(99) == "unknown status"
+
+
+def _params(**kw):
+    d = dict(temperature=1.0, top_k=20, top_p=0.95, min_p=0.0, presence_penalty=0.0, frequency_penalty=0.0,
+             repetition_penalty=1.0, seed=0)
+    d.update(kw)
+    return _lib.KlsParams(*d.values())
+
+
+def test_create_argument_errors():
+    L = _lib.lib()
+    h = C.c_void_p()
+    assert L.kls_create(None, 100, 1, C.byref(h)) == _lib.KLS_ERR_INVALID_ARG
+    p = _params()
+    assert L.kls_create(C.byref(p), 0, 1, C.byref(h)) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_create(C.byref(p), -5, 1, C.byref(h)) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_create(C.byref(p), 100, 0, C.byref(h)) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_create(C.byref(p), 100, 1, None) == _lib.KLS_ERR_INVALID_ARG
+    assert b"n_vocab" in L.kls_last_error() or b"max_rows" in L.kls_last_error() or L.kls_last_error()
+
+
+def test_null_handle_errors():
+    L = _lib.lib()
+    out = C.c_int32()
+    assert L.kls_destroy(None) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_reset(None) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_accept(None, 3) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_sample(None, None, 10, 0.5, C.byref(out)) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_verify(None, None, 4, None, None, None, None, None) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_sample_batch(None, None, 1, 10, None, None, None, None, None) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_get_candidates(None, 0, None, None, 0, None, None) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_debug_expf(0, 10, None, None) == _lib.KLS_ERR_INVALID_ARG
+
+
+def test_no_device_is_reported_without_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    L = _lib.lib()
+    h = C.c_void_p()
+    p = _params()
+    assert L.kls_create(C.byref(p), 1000, 4, C.byref(h)) == _lib.KLS_ERR_NO_DEVICE

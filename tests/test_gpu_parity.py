@@ -1,0 +1,281 @@
+"""GPU parity: the HIP path through the C ABI against the oracle (and the reference's golden tokens) on the same
+logits and uniforms. Token ids, top-k id lists, accepted counts: bit-exact. Probabilities: the stated bar is
+1e-5 relative; the tests assert bit equality, which the design guarantees (same operation order, correctly
+rounded f32/f64 operations, and an expf identical to the host libm's)."""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from klein_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    torch.cuda.init()
+    return torch
+
+
+@pytest.fixture(scope="module")
+def K():
+    import klein_amd
+    return klein_amd
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def check_row(S, O, row_logits, p, u, counts, label):
+    t, ids, probs, kept = O.sample(row_logits, p, u, counts, O.MODE_TOTAL)
+    gi, gp, gk, gkept = S.candidates(0)
+    return t, ids, probs, kept, gi, gp, gk, gkept
+
+
+def assert_same_candidates(O_ids, O_probs, O_kept, gi, gp, gk, gkept, label, k_expected=None):
+    n = len(O_ids)
+    if n <= 64:
+        assert gk == n, (label, gk, n)
+        assert list(gi) == list(O_ids), label
+        assert gp.tobytes() == O_probs.tobytes(), (label, np.max(np.abs(gp - O_probs) / np.maximum(O_probs, 1e-30)))
+        assert gkept == O_kept, label
+
+
+def test_expf_bitexact_vs_host_libm(torch_cuda, K, oracle_lib):
+    """The device expf against the host std::exp(float) on every float in [-110, 89]."""
+    torch = torch_cuda
+    L = oracle_lib.lib()
+    import ctypes as C
+    lo_neg = struct.unpack("<I", struct.pack("<f", -110.0))[0]
+    hi_pos = struct.unpack("<I", struct.pack("<f", 89.0))[0]
+    ranges = [(0x80000000, lo_neg), (0, hi_pos)]
+    chunk = 1 << 26
+    out = torch.empty(chunk, dtype=torch.float32, device="cuda")
+    bad = 0
+    for a, b in ranges:
+        say("expf range", hex(a), hex(b))
+        x = a
+        while x <= b:
+            n = min(chunk, b - x + 1)
+            K.debug_expf(x, out[:n])
+            h = out[:n].cpu().numpy()
+            first = C.c_uint32()
+            bad += L.orc_expf_compare(x, h.ctypes.data_as(C.POINTER(C.c_float)), n, 16, C.byref(first))
+            assert bad == 0, hex(first.value)
+            x += n
+    assert bad == 0
+
+
+@pytest.mark.parametrize("name", ["greedy", "topk_topp", "penalties"])
+def test_single_row_workloads(torch_cuda, K, oracle_lib, name):
+    torch = torch_cuda
+    O = oracle_lib
+    fx = json.load(open(os.path.join(GOLDEN, f"{name}.json")))
+    w = W.BUILDERS[name](seed=fx["seed"])
+    assert w.digest() == fx["logits_sha256"]
+    d = dev(torch, w.logits[0])
+    for case in fx["cases"]:
+        say(name, "seed", case["seed"])
+        p = W.Params(**{**fx["params"], "seed": case["seed"]})
+        S = K.Sampler(p, n_vocab=w.vocab)
+        if w.histories:
+            for t in w.histories[0]:
+                S.accept(int(t))
+        tok = S.sample(d)  # the sampler's own mt19937_64 draw, as the reference's
+        assert tok == case["token"], name
+        if name == "greedy":
+            assert tok == w.expected_greedy
+            continue
+        counts = W.counts_of(w.histories[0], w.vocab) if w.histories else None
+        t, ids, probs, kept = O.sample(w.logits[0], p, case["u"], counts, O.MODE_TOTAL)
+        gi, gp, gk, gkept = S.candidates(0)
+        assert t == tok
+        assert_same_candidates(ids, probs, kept, gi, gp, gk, gkept, name)
+        assert list(gi) == case["topk_ids"]
+        S.close()
+
+
+def test_host_pointer_input(torch_cuda, K, oracle_lib):
+    w = W.topk_topp()
+    S = K.Sampler(w.params, n_vocab=w.vocab)
+    for u in (0.0, 0.3, 0.999):
+        say("host pointer u", u)
+        assert S.sample(w.logits[0], u=u) == oracle_lib.sample(w.logits[0], w.params, u)[0]
+
+
+def test_verify_workload(torch_cuda, K, oracle_lib):
+    torch = torch_cuda
+    O = oracle_lib
+    fx = json.load(open(os.path.join(GOLDEN, "verify.json")))
+    w = W.verify(seed=fx["seed"])
+    assert w.digest() == fx["logits_sha256"]
+    d = dev(torch, w.logits)
+    seen = set()
+    for case in fx["cases"]:
+        say("verify seed", case["seed"], "drafts", case["drafts"])
+        p = W.Params(**{**fx["params"], "seed": case["seed"]})
+        S = K.Sampler(p, n_vocab=w.vocab)
+        toks, acc = S.verify(d, np.array(case["drafts"], np.int32))
+        assert acc == case["accepted"]
+        assert list(toks) == case["tokens"][:acc + 1]
+        seen.add(acc)
+        for r in range(acc + 1):
+            t, ids, probs, kept = O.sample(w.logits[r], p, case["u"][r], None, O.MODE_TOTAL)
+            gi, gp, gk, gkept = S.candidates(r)
+            assert_same_candidates(ids, probs, kept, gi, gp, gk, gkept, f"verify row {r}")
+        S.close()
+    assert seen == {0, 1, 2, 3}
+
+
+def test_batched_workload(torch_cuda, K, oracle_lib):
+    torch = torch_cuda
+    O = oracle_lib
+    fx = json.load(open(os.path.join(GOLDEN, "batched.json")))
+    w = W.batched(seed=fx["seed"])
+    assert w.digest() == fx["logits_sha256"]
+    d = dev(torch, w.logits)
+    off = np.zeros(w.rows + 1, np.int32)
+    off[1:] = np.cumsum([len(h) for h in w.histories])
+    ids = np.concatenate(w.histories).astype(np.int32)
+    u = np.array([c["u"] for c in fx["cases"]], dtype=np.float64)
+    p = W.Params(**fx["params"])
+    S = K.Sampler(p, n_vocab=w.vocab, max_rows=w.rows)
+    out = torch.full((w.rows,), -1, dtype=torch.int32, device="cuda")
+    say("batched 64 rows")
+    S.sample_batch(d, dev(torch, u), out, dev(torch, off), dev(torch, ids))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert list(got) == [c["token"] for c in fx["cases"]]
+    for r in range(0, w.rows, 9):
+        counts = W.counts_of(w.histories[r], w.vocab)
+        t, oids, probs, kept = O.sample(w.logits[r], p, u[r], counts, O.MODE_TOTAL)
+        gi, gp, gk, gkept = S.candidates(r)
+        assert t == got[r]
+        assert_same_candidates(oids, probs, kept, gi, gp, gk, gkept, f"batched row {r}")
+
+
+CASES = []
+_rng = np.random.default_rng(2026)
+for V in (1, 3, 64, 100, 1000, 1023, 1025, 4096, 8193, 50000, 248320):
+    for _ in range(3 if V < 248320 else 2):
+        T = float(_rng.choice([0.0, 0.3, 1.0, 2.0]))
+        k = int(_rng.choice([1, 2, 20, 63, 64]))
+        pen = int(_rng.integers(0, 3))
+        CASES.append((V, T, k, pen, int(_rng.integers(1, 2**31))))
+
+
+@pytest.mark.parametrize("V,T,k,pen,seed", CASES)
+def test_random_rows(torch_cuda, K, oracle_lib, V, T, k, pen, seed):
+    torch = torch_cuda
+    O = oracle_lib
+    rng = np.random.default_rng(seed)
+    kk = k if k < V else V
+    if T > 0 and kk > 64:
+        pytest.skip("k above 64")
+    x = (rng.standard_normal(V) * rng.uniform(0.5, 3)).astype(np.float32)
+    if V > 10:
+        x[rng.choice(V, min(V // 3, 40), replace=False)] = np.float32(rng.choice([2.5, 4.0]))  # exact ties
+        x[rng.choice(V, 3, replace=False)] = -0.0
+    pp = dict(temperature=T, top_k=k if rng.random() < 0.9 else 0, top_p=float(rng.choice([0.5, 0.9, 1.0])),
+              min_p=float(rng.choice([0.0, 0.05])))
+    if pen == 1:
+        pp.update(presence_penalty=0.5, frequency_penalty=0.2, repetition_penalty=1.1)
+    elif pen == 2:
+        pp.update(presence_penalty=-0.8, frequency_penalty=-0.1, repetition_penalty=0.7)
+    p = W.Params(**pp)
+    if T > 0 and not (0 < p.top_k < V) and V > 64:
+        p.top_k = k
+    hist = rng.integers(0, V, int(rng.integers(0, 600))).astype(np.int32) if pen else np.zeros(0, np.int32)
+    S = K.Sampler(p, n_vocab=V)
+    for t in hist:
+        S.accept(int(t))
+    counts = W.counts_of(hist, V) if pen else None
+    d = dev(torch, x)
+    for u in (0.0, float(rng.random()), 0.9999999):
+        say(V, T, k, pen, seed, u)
+        tok = S.sample(d, u=u)
+        t, ids, probs, kept = O.sample(x, p, u, counts, O.MODE_TOTAL)
+        assert tok == t
+        if T > 0:
+            gi, gp, gk, gkept = S.candidates(0)
+            assert_same_candidates(ids, probs, kept, gi, gp, gk, gkept, "random row")
+
+
+def test_all_equal_row(torch_cuda, K, oracle_lib):
+    torch = torch_cuda
+    V = 248320
+    x = np.full(V, 1.25, dtype=np.float32)
+    d = dev(torch, x)
+    assert K.Sampler(W.Params(temperature=0.0), n_vocab=V).sample(d) == 0
+    S = K.Sampler(W.Params(temperature=1.0, top_k=64, top_p=1.0), n_vocab=V)
+    say("all equal u=0.5")
+    tok = S.sample(d, u=0.5)
+    gi, gp, gk, _ = S.candidates(0)
+    assert list(gi) == list(range(64))
+    assert tok == oracle_lib.sample(x, S.params(), 0.5)[0]
+
+
+def test_greedy_inf_nan_edges(torch_cuda, K, oracle_lib):
+    torch = torch_cuda
+    V = 5000
+    S = K.Sampler(W.Params(temperature=0.0), n_vocab=V)
+    x = np.full(V, -np.inf, dtype=np.float32)
+    assert S.sample(dev(torch, x)) == 0
+    x[4000] = np.inf
+    x[4500] = np.inf
+    assert S.sample(dev(torch, x)) == 4000
+    x = np.full(V, np.nan, dtype=np.float32)
+    x[1234] = -3.0
+    assert S.sample(dev(torch, x)) == 1234
+
+
+def test_verify_penalized_sequence_graph_replay(torch_cuda, K, oracle_lib):
+    """An engine-like decode: 40 verify steps through the same captured graph, logits rewritten in place, with
+    penalties so row i must see the drafts d_1..d_i; history evolves through the emitted tokens."""
+    torch = torch_cuda
+    O = oracle_lib
+    V = 248320
+    rng = np.random.default_rng(77)
+    p = W.Params(temperature=0.8, top_k=20, top_p=0.9, presence_penalty=0.6, frequency_penalty=0.3,
+                 repetition_penalty=1.2, seed=99)
+    S = K.Sampler(p, n_vocab=V)
+    counts = np.zeros(V, np.int32)
+    for t in rng.integers(0, V, 300):
+        S.accept(int(t))
+        counts[t] += 1
+    buf = torch.empty((4, V), dtype=torch.float32, device="cuda")
+    from klein_amd.rng import MT19937_64, canonical
+    g = MT19937_64(99)
+    accs = []
+    for step in range(40):
+        x, _ = W._head_rows(rng, 4, V)
+        # drafts: the oracle's own tokens for a random prefix, so every accepted count occurs
+        u = np.array([canonical(g.copy()) for _ in range(1)])  # placeholder, replaced below
+        gp = g.copy()
+        u = np.array([canonical(gp) for _ in range(4)])
+        m = int(rng.integers(0, 4))
+        drafts = rng.integers(0, V, 3).astype(np.int32)
+        c = counts.copy()
+        for i in range(m):
+            drafts[i] = O.sample(x[i], p, u[i], c, O.MODE_TOTAL)[0]
+            c[drafts[i]] += 1
+        buf.copy_(torch.from_numpy(x))
+        say("verify step", step, "m", m)
+        toks, acc = S.verify(buf, drafts)
+        ot, oa, counts = O.verify(x, drafts, p, u, counts, O.MODE_TOTAL)
+        assert acc == oa and list(toks) == list(ot[:oa + 1]), step
+        g.discard(acc + 1)
+        accs.append(acc)
+    assert set(accs) == {0, 1, 2, 3}
