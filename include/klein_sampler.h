@@ -77,6 +77,14 @@ int kls_sample(kls_handle h, const float* logits, int n_vocab, double u, int32_t
 int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
                int32_t* out_tokens, int32_t* out_accepted, kls_stream stream);
 
+/* The two halves of kls_verify, for callers that overlap other host work with the step or bracket it with
+ * stream events: kls_verify_enqueue launches the step on `stream` and returns; kls_verify_wait waits for its
+ * results (spinning on the pinned result block) and then behaves as the end of kls_verify. One step may be in
+ * flight per handle. No counterpart in the reference, whose loop is synchronous. */
+int kls_verify_enqueue(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
+                       kls_stream stream);
+int kls_verify_wait(kls_handle h, int32_t* out_tokens, int32_t* out_accepted);
+
 /* Batched sampling of n_rows independent rows, all on the device, asynchronous on `stream` (no host sync).
  * Row r is at d_logits + r*row_stride floats; its token history is d_hist_ids[d_hist_off[r] .. d_hist_off[r+1])
  * (raw ids, repeats counted; d_hist_off has n_rows+1 entries; NULL offsets = no history). d_u[r] is row r's

@@ -18,7 +18,8 @@ KLS_ERR_NO_DEVICE = 5
 KLS_ERR_OOM = 6
 
 # every entry point include/klein_sampler.h declares
-EXPORTS = ["kls_create", "kls_destroy", "kls_reset", "kls_accept", "kls_sample", "kls_verify", "kls_sample_batch",
+EXPORTS = ["kls_create", "kls_destroy", "kls_reset", "kls_accept", "kls_sample", "kls_verify", "kls_verify_enqueue",
+           "kls_verify_wait", "kls_sample_batch",
            "kls_get_candidates", "kls_debug_expf", "kls_status_string", "kls_last_error"]
 
 
@@ -51,6 +52,8 @@ def lib():
         L.kls_accept.argtypes = [P, C.c_int32]
         L.kls_sample.argtypes = [P, C.c_void_p, C.c_int, C.c_double, I32P]
         L.kls_verify.argtypes = [P, C.c_void_p, C.c_int, I32P, F64P, I32P, I32P, C.c_void_p]
+        L.kls_verify_enqueue.argtypes = [P, C.c_void_p, C.c_int, I32P, F64P, C.c_void_p]
+        L.kls_verify_wait.argtypes = [P, I32P, I32P]
         L.kls_sample_batch.argtypes = [P, C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_void_p, C.c_void_p]
         L.kls_get_candidates.argtypes = [P, C.c_int, I32P, F32P, C.c_int, I32P, I32P]

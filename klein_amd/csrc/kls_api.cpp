@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -51,7 +52,7 @@ struct kls_sampler {
     int k = 0;
     int V = 0, max_rows = 0, device = 0;
     int bucket_shift = MIN_BUCKET_SHIFT, n_buckets = 0;
-    int seg_len_override = 0, target_wg = 256;
+    int seg_len_override = 0, target_wg = 300, hist_parts = 4, share_min_wg = 1024;
     hipStream_t stream = nullptr;
 
     // token history: host copy (as the reference's counts_) + what has reached the device
@@ -71,9 +72,7 @@ struct kls_sampler {
     uint64_t* d_seg_cand = nullptr;
     uint32_t* d_row_ticket = nullptr;
     uint64_t* d_row_thr = nullptr;
-    uint32_t* d_step_ticket = nullptr;
     int32_t* d_tokens = nullptr;
-    int32_t* d_accepted = nullptr;
     uint64_t* d_dbg_keys = nullptr;
     float* d_dbg_probs = nullptr;
     int32_t* d_dbg_meta = nullptr;
@@ -85,11 +84,15 @@ struct kls_sampler {
     ResultBlock* res = nullptr;
     CallBlock* call_dev = nullptr;  // device views of the same mapped memory
     ResultBlock* res_dev = nullptr;
+    int32_t tokens[VERIFY_MAX_ROWS] = {};  // tokens of the last completed step
     uint32_t seq = 0;
 
     // verify graph, keyed by what it bakes in
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
+    bool inflight = false;
+    hipStream_t inflight_stream = nullptr;
+    int inflight_rows = 0;
     const float* g_logits = nullptr;
     int g_rows = 0;
     bool g_valid = false;
@@ -107,19 +110,17 @@ bool is_device_ptr(const void* p) {
     return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
-void segments_for(const kls_sampler* h, int rows, bool penalize, int* seg_len, int* segs) {
-    const int bw = 1 << h->bucket_shift;
-    long long sl = h->seg_len_override;
-    if (sl <= 0) {
-        const long long per = ((long long) h->V * rows + h->target_wg - 1) / h->target_wg;
-        sl = per;
+// Segment length: 256 threads x {4, 8, 16, 32} logits. The smallest length whose grid (rows x segments) stays
+// within the target workgroup count, so small batches spread over every CU and large ones keep long segments.
+void segments_for(const kls_sampler* h, int rows, int* seg_len, int* segs) {
+    int sl = SEG_MIN;
+    if (h->seg_len_override >= SEG_MIN && h->seg_len_override <= SEG_MAX) {
+        sl = h->seg_len_override;
+    } else {
+        while (sl < SEG_MAX && (long long) rows * ((h->V + sl - 1) / sl) > h->target_wg) sl *= 2;
     }
-    sl = ((sl + bw - 1) / bw) * bw;
-    sl = std::max<long long>(sl, bw);
-    if (penalize) sl = std::min<long long>(sl, SEG_MAX_PENALIZED);
-    sl = std::min<long long>(sl, ((long long) h->V + bw - 1) / bw * bw);
-    *seg_len = (int) sl;
-    *segs = (int) ((h->V + sl - 1) / sl);
+    *seg_len = sl;
+    *segs = (h->V + sl - 1) / sl;
 }
 
 // Rebuilds the device history from the host counts (bucketed unique ids + counts) and clears `pending`.
@@ -155,14 +156,14 @@ RowsArgs base_args(kls_sampler* h, const float* logits, int rows, int64_t stride
     a.row_stride = stride;
     a.V = h->V;
     a.n_rows = rows;
-    segments_for(h, rows, h->penalize, &a.seg_len, &a.segs);
+    segments_for(h, rows, &a.seg_len, &a.segs);
     a.p = h->sp;
     a.bucket_shift = h->bucket_shift;
     a.n_buckets = h->n_buckets;
     a.seg_cand = h->d_seg_cand;
     a.row_ticket = h->d_row_ticket;
     a.row_thr = h->d_row_thr;
-    a.step_ticket = h->d_step_ticket;
+    a.share_bounds = (long long) rows * a.segs > h->share_min_wg ? 1 : 0;
     a.out_tokens = h->d_tokens;
     a.dbg_keys = h->d_dbg_keys;
     a.dbg_probs = h->d_dbg_probs;
@@ -180,14 +181,13 @@ RowsArgs step_args(kls_sampler* h, const float* logits, int rows, bool verify) {
         a.hist_boff = h->d_hist_boff;
         a.hist_cap = h->V;
         a.hist_shared = 1;
+        a.hist_parts = 1;
         a.extra_a = h->call_dev->pending;
         a.extra_a_n = &h->call_dev->n_pending;
         a.extra_b = verify ? h->call_dev->drafts : nullptr;
         a.extra_b_step = verify ? 1 : 0;
     }
     a.u = h->call_dev->u;
-    a.drafts = verify ? h->call_dev->drafts : nullptr;
-    a.out_accepted = h->d_accepted;
     a.host_res = h->res_dev;
     a.call = h->call_dev;
     return a;
@@ -210,8 +210,9 @@ int prepare_history(kls_sampler* h, hipStream_t s) {
     return KLS_OK;
 }
 
-// Launches one step over `rows` rows of the handle's history and waits for the results in the pinned block.
-int run_step(kls_sampler* h, const float* logits, int rows, bool verify, hipStream_t s) {
+// Enqueues one step over `rows` rows of the handle's history on `s`; results land in the pinned block.
+int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hipStream_t s) {
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is already in flight on this handle");
     const float* dl = logits;
     if (!is_device_ptr(logits)) {
         KLS_HIP(hipMemcpyAsync(h->d_rows_buf, logits, sizeof(float) * (size_t) rows * h->V, hipMemcpyHostToDevice, s));
@@ -220,7 +221,6 @@ int run_step(kls_sampler* h, const float* logits, int rows, bool verify, hipStre
     int st = prepare_history(h, s);
     if (st) return st;
     h->call->seq = ++h->seq;
-    h->res->seq = 0;
     const RowsArgs a = step_args(h, dl, rows, verify);
     if (verify) {
         if (!h->g_valid || h->g_logits != dl || h->g_rows != rows) {
@@ -245,8 +245,38 @@ int run_step(kls_sampler* h, const float* logits, int rows, bool verify, hipStre
     } else {
         KLS_HIP(launch_rows(a, h->greedy, h->penalize, s));
     }
-    KLS_HIP(hipStreamSynchronize(s));
-    if (h->res->seq != h->call->seq) return fail(KLS_ERR_HIP, "step result not published");
+    h->inflight = true;
+    h->inflight_stream = s;
+    h->inflight_rows = rows;
+    return KLS_OK;
+}
+
+// Waits for the in-flight step: spins on the per-row sequence numbers the kernel publishes after each row's
+// token, falling back to a stream synchronization after 50 ms (queued work ahead of the step, or a failure).
+int wait_step(kls_sampler* h) {
+    if (!h->inflight) return fail(KLS_ERR_INVALID_ARG, "no step in flight on this handle");
+    h->inflight = false;
+    const uint32_t want = h->call->seq;
+    const int rows = h->inflight_rows;
+    auto done = [&] {
+        for (int r = 0; r < rows; ++r) {
+            const uint64_t w = __atomic_load_n(&h->res->row_word[r], __ATOMIC_ACQUIRE);
+            if ((uint32_t) (w >> 32) != want) return false;
+            h->tokens[r] = (int32_t) (uint32_t) w;
+        }
+        return true;
+    };
+    const auto t0 = std::chrono::steady_clock::now();
+    while (!done()) {
+        if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(50)) {
+            KLS_HIP(hipStreamSynchronize(h->inflight_stream));
+            if (!done()) return fail(KLS_ERR_HIP, "step result not published");
+            break;
+        }
+#if defined(__x86_64__)
+        __builtin_ia32_pause();
+#endif
+    }
     return KLS_OK;
 }
 
@@ -281,7 +311,7 @@ int kls_destroy(kls_handle h) {
     if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
     if (h->graph) (void) hipGraphDestroy(h->graph);
     void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_part_ids, h->d_part_boff, h->d_seg_cand,
-                   h->d_row_ticket, h->d_row_thr, h->d_step_ticket, h->d_tokens, h->d_accepted, h->d_dbg_keys,
+                   h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_dbg_keys,
                    h->d_dbg_probs, h->d_dbg_meta, h->d_rows_buf};
     for (void* p : dev)
         if (p) (void) hipFree(p);
@@ -320,6 +350,8 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     h->n_buckets = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;
     if (const char* e = getenv("KLS_SEG_LEN")) h->seg_len_override = atoi(e);
     if (const char* e = getenv("KLS_TARGET_WG")) h->target_wg = std::max(1, atoi(e));
+    if (const char* e = getenv("KLS_SHARE_MIN_WG")) h->share_min_wg = atoi(e);
+    if (const char* e = getenv("KLS_HIST_PARTS")) h->hist_parts = std::min(64, std::max(1, atoi(e)));
     (void) hipGetDevice(&h->device);
 
     auto oom = [&](const char* what, hipError_t e) {
@@ -328,7 +360,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     };
     hipError_t e;
     if ((e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking)) != hipSuccess) return oom("stream", e);
-    h->max_segs = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;  // smallest segment = one bucket
+    h->max_segs = (n_vocab + SEG_MIN - 1) / SEG_MIN;
     const size_t R = (size_t) max_rows;
     h->part_cap = (int) std::min<size_t>(R * BATCH_HISTORY_PER_ROW, 1u << 30);
 #define ALLOC(ptr, bytes) \
@@ -337,13 +369,11 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     ALLOC(h->d_hist_w, sizeof(int32_t) * n_vocab);
     ALLOC(h->d_hist_boff, sizeof(int32_t) * (h->n_buckets + 1));
     ALLOC(h->d_part_ids, sizeof(int32_t) * (size_t) h->part_cap);
-    ALLOC(h->d_part_boff, sizeof(int32_t) * R * (h->n_buckets + 1));
+    ALLOC(h->d_part_boff, sizeof(int32_t) * R * h->hist_parts * (h->n_buckets + 1));
     ALLOC(h->d_seg_cand, sizeof(uint64_t) * R * h->max_segs * KCAP);
     ALLOC(h->d_row_ticket, sizeof(uint32_t) * R);
     ALLOC(h->d_row_thr, sizeof(uint64_t) * R);
-    ALLOC(h->d_step_ticket, sizeof(uint32_t));
     ALLOC(h->d_tokens, sizeof(int32_t) * R);
-    ALLOC(h->d_accepted, sizeof(int32_t));
     ALLOC(h->d_dbg_keys, sizeof(uint64_t) * R * KCAP);
     ALLOC(h->d_dbg_probs, sizeof(float) * R * KCAP);
     ALLOC(h->d_dbg_meta, sizeof(int32_t) * R * 2);
@@ -365,7 +395,6 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     // zero the self-resetting counters and bounds once; the kernels leave them zero after every launch
     if ((e = hipMemsetAsync(h->d_row_ticket, 0, sizeof(uint32_t) * R, h->stream)) != hipSuccess) return oom("init", e);
     if ((e = hipMemsetAsync(h->d_row_thr, 0, sizeof(uint64_t) * R, h->stream)) != hipSuccess) return oom("init", e);
-    if ((e = hipMemsetAsync(h->d_step_ticket, 0, sizeof(uint32_t), h->stream)) != hipSuccess) return oom("init", e);
     if ((e = hipMemsetAsync(h->d_hist_boff, 0, sizeof(int32_t) * (h->n_buckets + 1), h->stream)) != hipSuccess)
         return oom("init", e);
     if ((e = hipStreamSynchronize(h->stream)) != hipSuccess) return oom("init", e);
@@ -394,33 +423,49 @@ int kls_sample(kls_handle h, const float* logits, int n_vocab, double u, int32_t
     if (n_vocab != h->V) return fail(KLS_ERR_INVALID_ARG, "n_vocab differs from the handle's");
     (void) hipSetDevice(h->device);
     h->call->u[0] = u;
-    const int st = run_step(h, logits, 1, false, h->stream);
+    int st = enqueue_step(h, logits, 1, false, h->stream);
+    if (!st) st = wait_step(h);
     if (st) return st;
-    *out_token = h->res->tokens[0];
+    *out_token = h->tokens[0];
     return KLS_OK;
 }
 
-int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
-               int32_t* out_tokens, int32_t* out_accepted, kls_stream stream) {
+int kls_verify_enqueue(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
+                       kls_stream stream) {
     if (int st = check_handle(h)) return st;
-    if (!logits || !u || !out_tokens || !out_accepted || (nb > 1 && !drafts))
-        return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (!logits || !u || (nb > 1 && !drafts)) return fail(KLS_ERR_INVALID_ARG, "null argument");
     if (nb < 1) return fail(KLS_ERR_INVALID_ARG, "nb must be at least 1");
     if (nb > h->max_rows || nb > VERIFY_MAX_ROWS) return fail(KLS_ERR_RANGE, "nb above the handle's capacity");
     (void) hipSetDevice(h->device);
     hipStream_t s = stream ? (hipStream_t) stream : h->stream;
     for (int i = 0; i < nb; ++i) h->call->u[i] = u[i];
     for (int i = 0; i + 1 < nb; ++i) h->call->drafts[i] = drafts[i];
-    const int st = run_step(h, logits, nb, true, s);
-    if (st) return st;
-    const int acc = h->res->accepted;
+    return enqueue_step(h, logits, nb, true, s);
+}
+
+int kls_verify_wait(kls_handle h, int32_t* out_tokens, int32_t* out_accepted) {
+    if (int st = check_handle(h)) return st;
+    if (!out_tokens || !out_accepted) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    const int nb = h->inflight_rows;
+    if (int st = wait_step(h)) return st;
+    // engine.cpp:571-573: draft i+1 is accepted while it equals the token sampled at position i
+    int acc = 0;
+    while (acc < nb - 1 && h->tokens[acc] == h->call->drafts[acc]) ++acc;
     for (int i = 0; i <= acc; ++i) {
-        out_tokens[i] = h->res->tokens[i];
+        out_tokens[i] = h->tokens[i];
         add_history(h, out_tokens[i]);
     }
-    for (int i = acc + 1; i < nb; ++i) out_tokens[i] = h->res->tokens[i];
+    for (int i = acc + 1; i < nb; ++i) out_tokens[i] = h->tokens[i];
     *out_accepted = acc;
     return KLS_OK;
+}
+
+int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
+               int32_t* out_tokens, int32_t* out_accepted, kls_stream stream) {
+    if (int st = check_handle(h)) return st;
+    if (!out_tokens || !out_accepted) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (int st = kls_verify_enqueue(h, logits, nb, drafts, u, stream)) return st;
+    return kls_verify_wait(h, out_tokens, out_accepted);
 }
 
 int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_hist_off,
@@ -436,12 +481,12 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
     hipStream_t s = stream ? (hipStream_t) stream : h->stream;
     RowsArgs a = base_args(h, d_logits, n_rows, row_stride);
     const bool pen = h->penalize && d_hist_off != nullptr;
-    if (!pen) segments_for(h, n_rows, false, &a.seg_len, &a.segs);
     if (pen) {
         PartitionArgs pa{};
         pa.hist_off = d_hist_off;
         pa.hist_ids = d_hist_ids;
         pa.n_rows = n_rows;
+        pa.parts = h->hist_parts;
         pa.V = h->V;
         pa.bucket_shift = h->bucket_shift;
         pa.n_buckets = h->n_buckets;
@@ -453,6 +498,7 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
         a.hist_boff = h->d_part_boff;
         a.hist_cap = h->part_cap;
         a.hist_shared = 0;
+        a.hist_parts = h->hist_parts;
     }
     a.u = d_u;
     a.out_tokens = d_out_tokens;

@@ -12,8 +12,10 @@ constexpr int KCAP = 64;
 constexpr int VERIFY_MAX_ROWS = 16;
 // History ids accepted since the last device upload that ride along with a call.
 constexpr int PENDING_CAP = 256;
-// Largest segment (vocabulary ids per workgroup) when penalties are on: its counts live in LDS (4 B per id).
-constexpr int SEG_MAX_PENALIZED = 8192;
+// Segments (vocabulary ids per workgroup) are 256 threads x EPT elements, EPT in {4, 8, 16, 32}; with
+// penalties the segment's history counts live in LDS (4 B per id).
+constexpr int SEG_MIN = 1024;
+constexpr int SEG_MAX = 8192;
 // History bucket width: history lists are partitioned into buckets of (1 << bucket_shift) ids, and segments
 // start on bucket boundaries so a workgroup finds its history slice with two loads.
 constexpr int MIN_BUCKET_SHIFT = 10;
@@ -28,11 +30,10 @@ struct CallBlock {
     int32_t pending[PENDING_CAP];
 };
 
-// Results a step writes back to pinned host memory.
+// Results a step writes back to pinned host memory: per row one 64-bit word, (sequence number << 32) | token,
+// stored at once so the host sees either the old word or the new one.
 struct ResultBlock {
-    int32_t tokens[VERIFY_MAX_ROWS];
-    int32_t accepted;
-    uint32_t seq;
+    uint64_t row_word[VERIFY_MAX_ROWS];
 };
 
 struct SamplingParams {
@@ -57,9 +58,10 @@ struct RowsArgs {
     // history: per row (or shared) bucketed id list with optional weights (counts); NULL hist_boff = none
     const int32_t* hist_ids;
     const int32_t* hist_w;     // NULL: every entry counts once
-    const int32_t* hist_boff;  // [rows or 1][n_buckets + 1] absolute offsets into hist_ids
+    const int32_t* hist_boff;  // [rows or 1][hist_parts][n_buckets + 1] absolute offsets into hist_ids
     int32_t hist_cap;          // entries of hist_ids that may be read
-    int32_t hist_shared;       // 1: all rows use the first bucket-offset row
+    int32_t hist_shared;       // 1: all rows use the first row of bucket offsets
+    int32_t hist_parts;        // independently bucketed parts per row
     int32_t bucket_shift;
     int32_t n_buckets;
     // extra history ids counted on top: list A (count read from memory) for every row, list B's first
@@ -75,30 +77,28 @@ struct RowsArgs {
     uint64_t* seg_cand;     // [n_rows][segs][KCAP]
     uint32_t* row_ticket;   // [n_rows]
     uint64_t* row_thr;      // [n_rows]
-    uint32_t* step_ticket;  // [1]
+    int32_t share_bounds;   // publish / read per-row lower bounds across workgroups (large grids)
 
     // outputs
     int32_t* out_tokens;    // [n_rows] device
     uint64_t* dbg_keys;     // [n_rows][KCAP] final sorted candidate keys
     float* dbg_probs;       // [n_rows][KCAP]
     int32_t* dbg_meta;      // [n_rows][2]: k, kept
-    // verify step (NULL drafts: no accept computation)
-    const int32_t* drafts;  // [n_rows-1]
-    int32_t* out_accepted;  // device
-    ResultBlock* host_res;  // pinned, may be NULL
-    const CallBlock* call;  // for the sequence number, may be NULL
+    ResultBlock* host_res;  // pinned, may be NULL: tokens and per-row sequence numbers for the host
+    const CallBlock* call;  // the sequence number to publish (with host_res)
 };
 
 struct PartitionArgs {
     const int32_t* hist_off;  // [n_rows + 1]
     const int32_t* hist_ids;
     int32_t n_rows;
+    int32_t parts;            // workgroups per row; part p covers the p-th slice of the row's ids
     int32_t V;
     int32_t bucket_shift;
     int32_t n_buckets;
     int32_t cap;              // entries of part_ids (offsets are clamped to it)
     int32_t* part_ids;        // same indexing as hist_ids
-    int32_t* boff;            // [n_rows][n_buckets + 1]
+    int32_t* boff;            // [n_rows][parts][n_buckets + 1]
 };
 
 // Launchers (kls_kernels.hip). Return hipSuccess or the launch error.
