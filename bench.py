@@ -58,6 +58,28 @@ def traffic_from_profiles():
     return None
 
 
+def copy_probe(torch, stream):
+    """A plain device copy of 256 MiB (torch's copy kernel): its measured rate, and the reference size that the
+    HBM byte counters of the same run are calibrated against."""
+    n = 256 * 1024 * 1024 // 4
+    a = torch.empty(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    for _ in range(3):
+        b.copy_(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(10):
+        b.copy_(a)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / 10
+    del a, b
+    return {"bytes_read": n * 4, "bytes_written": n * 4, "us": round(us, 2),
+            "GBps_read_plus_write": round(2 * n * 4 / (us * 1e-6) / 1e9, 1)}
+
+
 def cpu_baseline(w, seconds):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
@@ -226,6 +248,7 @@ def main():
                           "GBps_hot": round(BATCH_BYTES / (res["hot"] * 1e-6) / 1e9, 1)}
         SB.close()
 
+    out["copy_probe"] = copy_probe(torch, stream)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
     print(json.dumps(out), flush=True)
