@@ -87,9 +87,10 @@ int kls_verify_wait(kls_handle h, int32_t* out_tokens, int32_t* out_accepted);
 
 /* Batched sampling of n_rows independent rows, all on the device, asynchronous on `stream` (no host sync).
  * Row r is at d_logits + r*row_stride floats; its token history is d_hist_ids[d_hist_off[r] .. d_hist_off[r+1])
- * (raw ids, repeats counted; d_hist_off has n_rows+1 entries; NULL offsets = no history). d_u[r] is row r's
- * uniform. Tokens are written to d_out_tokens[r]. The handle's own history is not used or changed. Each row
- * equals one Sampler::sample call on that row after accept() of its history ids. */
+ * (raw ids, repeats counted, ids outside [0, n_vocab) ignored; d_hist_off has n_rows+1 non-decreasing entries
+ * that index d_hist_ids; NULL offsets = no history). d_u[r] is row r's uniform. Tokens are written to
+ * d_out_tokens[r]. The handle's own history is not used or changed. Each row equals one Sampler::sample call on
+ * that row after accept() of its history ids. */
 int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_hist_off,
                      const int32_t* d_hist_ids, const double* d_u, int32_t* d_out_tokens, kls_stream stream);
 

@@ -41,8 +41,6 @@ int fail(int status, const char* what, hipError_t e = hipSuccess) {
         if (e_ != hipSuccess) return fail(KLS_ERR_HIP, #expr, e_);           \
     } while (0)
 
-constexpr int BATCH_HISTORY_PER_ROW = 65536;  // raw history ids per row the batch entry point can take
-
 }  // namespace
 
 struct kls_sampler {
@@ -52,7 +50,7 @@ struct kls_sampler {
     int k = 0;
     int V = 0, max_rows = 0, device = 0;
     int bucket_shift = MIN_BUCKET_SHIFT, n_buckets = 0;
-    int seg_len_override = 0, target_wg = 300, hist_parts = 4, share_min_wg = 1024;
+    int seg_len_override = 0, target_wg = 300, share_min_wg = 1024, xcd_map = 1;
     hipStream_t stream = nullptr;
 
     // token history: host copy (as the reference's counts_) + what has reached the device
@@ -62,11 +60,6 @@ struct kls_sampler {
     int32_t* d_hist_w = nullptr;    // [V] counts
     int32_t* d_hist_boff = nullptr; // [n_buckets + 1]
     int32_t* h_stage = nullptr;     // pinned staging for uploads: 2*V + n_buckets + 1
-
-    // batch history partition
-    int32_t* d_part_ids = nullptr;  // [max_rows * BATCH_HISTORY_PER_ROW]
-    int32_t* d_part_boff = nullptr; // [max_rows][n_buckets + 1]
-    int part_cap = 0;
 
     // scratch
     uint64_t* d_seg_cand = nullptr;
@@ -164,6 +157,7 @@ RowsArgs base_args(kls_sampler* h, const float* logits, int rows, int64_t stride
     a.row_ticket = h->d_row_ticket;
     a.row_thr = h->d_row_thr;
     a.share_bounds = (long long) rows * a.segs > h->share_min_wg ? 1 : 0;
+    a.xcd_map = h->xcd_map;
     a.out_tokens = h->d_tokens;
     a.dbg_keys = h->d_dbg_keys;
     a.dbg_probs = h->d_dbg_probs;
@@ -179,9 +173,7 @@ RowsArgs step_args(kls_sampler* h, const float* logits, int rows, bool verify) {
         a.hist_ids = h->d_hist_ids;
         a.hist_w = h->d_hist_w;
         a.hist_boff = h->d_hist_boff;
-        a.hist_cap = h->V;
-        a.hist_shared = 1;
-        a.hist_parts = 1;
+
         a.extra_a = h->call_dev->pending;
         a.extra_a_n = &h->call_dev->n_pending;
         a.extra_b = verify ? h->call_dev->drafts : nullptr;
@@ -310,7 +302,7 @@ int kls_destroy(kls_handle h) {
     if (h->stream) (void) hipStreamSynchronize(h->stream);
     if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
     if (h->graph) (void) hipGraphDestroy(h->graph);
-    void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_part_ids, h->d_part_boff, h->d_seg_cand,
+    void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_seg_cand,
                    h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_dbg_keys,
                    h->d_dbg_probs, h->d_dbg_meta, h->d_rows_buf};
     for (void* p : dev)
@@ -351,7 +343,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     if (const char* e = getenv("KLS_SEG_LEN")) h->seg_len_override = atoi(e);
     if (const char* e = getenv("KLS_TARGET_WG")) h->target_wg = std::max(1, atoi(e));
     if (const char* e = getenv("KLS_SHARE_MIN_WG")) h->share_min_wg = atoi(e);
-    if (const char* e = getenv("KLS_HIST_PARTS")) h->hist_parts = std::min(64, std::max(1, atoi(e)));
+    if (const char* e = getenv("KLS_XCD_MAP")) h->xcd_map = atoi(e) != 0;
     (void) hipGetDevice(&h->device);
 
     auto oom = [&](const char* what, hipError_t e) {
@@ -362,14 +354,11 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     if ((e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking)) != hipSuccess) return oom("stream", e);
     h->max_segs = (n_vocab + SEG_MIN - 1) / SEG_MIN;
     const size_t R = (size_t) max_rows;
-    h->part_cap = (int) std::min<size_t>(R * BATCH_HISTORY_PER_ROW, 1u << 30);
 #define ALLOC(ptr, bytes) \
     if ((e = hipMalloc((void**) &(ptr), (bytes))) != hipSuccess) return oom(#ptr, e)
     ALLOC(h->d_hist_ids, sizeof(int32_t) * n_vocab);
     ALLOC(h->d_hist_w, sizeof(int32_t) * n_vocab);
     ALLOC(h->d_hist_boff, sizeof(int32_t) * (h->n_buckets + 1));
-    ALLOC(h->d_part_ids, sizeof(int32_t) * (size_t) h->part_cap);
-    ALLOC(h->d_part_boff, sizeof(int32_t) * R * h->hist_parts * (h->n_buckets + 1));
     ALLOC(h->d_seg_cand, sizeof(uint64_t) * R * h->max_segs * KCAP);
     ALLOC(h->d_row_ticket, sizeof(uint32_t) * R);
     ALLOC(h->d_row_thr, sizeof(uint64_t) * R);
@@ -482,23 +471,8 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
     RowsArgs a = base_args(h, d_logits, n_rows, row_stride);
     const bool pen = h->penalize && d_hist_off != nullptr;
     if (pen) {
-        PartitionArgs pa{};
-        pa.hist_off = d_hist_off;
-        pa.hist_ids = d_hist_ids;
-        pa.n_rows = n_rows;
-        pa.parts = h->hist_parts;
-        pa.V = h->V;
-        pa.bucket_shift = h->bucket_shift;
-        pa.n_buckets = h->n_buckets;
-        pa.cap = h->part_cap;
-        pa.part_ids = h->d_part_ids;
-        pa.boff = h->d_part_boff;
-        KLS_HIP(launch_partition(pa, s));
-        a.hist_ids = h->d_part_ids;
-        a.hist_boff = h->d_part_boff;
-        a.hist_cap = h->part_cap;
-        a.hist_shared = 0;
-        a.hist_parts = h->hist_parts;
+        a.hist_ids = d_hist_ids;
+        a.hist_off = d_hist_off;
     }
     a.u = d_u;
     a.out_tokens = d_out_tokens;

@@ -52,16 +52,18 @@ struct RowsArgs {
     int32_t V;
     int32_t n_rows;
     int32_t segs;
-    int32_t seg_len;  // multiple of the history bucket width
+    int32_t seg_len;  // 256 * EPT
+    int32_t xcd_map;  // 1: deal (row, segment) work so that a row's segments run on one XCD (see the kernel)
     SamplingParams p;
 
-    // history: per row (or shared) bucketed id list with optional weights (counts); NULL hist_boff = none
+    // history, one of two forms (neither: no history):
+    //  * bucketed (the handle's own history, shared by all rows): unique ids sorted into buckets of
+    //    (1 << bucket_shift) ids with counts hist_w; hist_boff[b] = first entry of bucket b;
+    //  * raw (the batch entry point): row r's ids are hist_ids[hist_off[r] .. hist_off[r+1]), repeats counted.
     const int32_t* hist_ids;
-    const int32_t* hist_w;     // NULL: every entry counts once
-    const int32_t* hist_boff;  // [rows or 1][hist_parts][n_buckets + 1] absolute offsets into hist_ids
-    int32_t hist_cap;          // entries of hist_ids that may be read
-    int32_t hist_shared;       // 1: all rows use the first row of bucket offsets
-    int32_t hist_parts;        // independently bucketed parts per row
+    const int32_t* hist_w;     // bucketed form: counts
+    const int32_t* hist_boff;  // bucketed form: [n_buckets + 1]
+    const int32_t* hist_off;   // raw form: [n_rows + 1]
     int32_t bucket_shift;
     int32_t n_buckets;
     // extra history ids counted on top: list A (count read from memory) for every row, list B's first
@@ -88,22 +90,10 @@ struct RowsArgs {
     const CallBlock* call;  // the sequence number to publish (with host_res)
 };
 
-struct PartitionArgs {
-    const int32_t* hist_off;  // [n_rows + 1]
-    const int32_t* hist_ids;
-    int32_t n_rows;
-    int32_t parts;            // workgroups per row; part p covers the p-th slice of the row's ids
-    int32_t V;
-    int32_t bucket_shift;
-    int32_t n_buckets;
-    int32_t cap;              // entries of part_ids (offsets are clamped to it)
-    int32_t* part_ids;        // same indexing as hist_ids
-    int32_t* boff;            // [n_rows][parts][n_buckets + 1]
-};
 
 // Launchers (kls_kernels.hip). Return hipSuccess or the launch error.
 hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_t s);
-hipError_t launch_partition(const PartitionArgs& a, hipStream_t s);
+int rows_grid(const RowsArgs& a);  // workgroups launch_rows starts
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s);
 
 }  // namespace kls

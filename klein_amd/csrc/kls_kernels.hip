@@ -261,19 +261,36 @@ __device__ __forceinline__ float penalize(float l, uint32_t c, const SamplingPar
 // Counts the history ids that fall in [lo, hi) into the LDS table s_cnt[0 .. hi-lo).
 __device__ __forceinline__ void stage_history(const RowsArgs& a, int row, int lo, int hi) {
     const int tid = threadIdx.x;
-    for (int i = tid; i < hi - lo; i += WG) s_cnt[i] = 0u;
+    const int n4 = (hi - lo + 3) & ~3;  // <= seg_len: the table is zeroed in 16-byte stores
+    for (int i = 4 * tid; i < n4; i += 4 * WG) *reinterpret_cast<uint4*>(s_cnt + i) = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     if (a.hist_boff) {
+        // bucketed unique ids with counts: read the buckets that overlap [lo, hi)
         const int b0 = lo >> a.bucket_shift;
         const int b1 = min(a.n_buckets, (hi + (1 << a.bucket_shift) - 1) >> a.bucket_shift);
-        for (int part = 0; part < a.hist_parts; ++part) {
-            const int32_t* bo =
-                a.hist_boff + ((int64_t) (a.hist_shared ? 0 : row) * a.hist_parts + part) * (a.n_buckets + 1);
-            const int s0 = max(bo[b0], 0), s1 = min(bo[b1], a.hist_cap);
-            for (int j = s0 + tid; j < s1; j += WG) {
-                const int id = a.hist_ids[j];
-                if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], a.hist_w ? (uint32_t) a.hist_w[j] : 1u);
-            }
+        const int s0 = max(a.hist_boff[b0], 0), s1 = a.hist_boff[b1];
+        for (int j = s0 + tid; j < s1; j += WG) {
+            const int id = a.hist_ids[j];
+            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], (uint32_t) a.hist_w[j]);
+        }
+    } else if (a.hist_off) {
+        // raw ids of this row: every workgroup of the row scans them (from L2) and keeps those in its segment
+        const int s0 = max(a.hist_off[row], 0), s1 = a.hist_off[row + 1];
+        const int head = min(s1, (s0 + 3) & ~3), body = head + (max(s1 - head, 0) & ~3);
+        for (int j = s0 + tid; j < head; j += WG) {
+            const int id = a.hist_ids[j];
+            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], 1u);
+        }
+        for (int j = head + 4 * tid; j < body; j += 4 * WG) {
+            const int4 q = *reinterpret_cast<const int4*>(a.hist_ids + j);
+            if (q.x >= lo && q.x < hi) atomicAdd(&s_cnt[q.x - lo], 1u);
+            if (q.y >= lo && q.y < hi) atomicAdd(&s_cnt[q.y - lo], 1u);
+            if (q.z >= lo && q.z < hi) atomicAdd(&s_cnt[q.z - lo], 1u);
+            if (q.w >= lo && q.w < hi) atomicAdd(&s_cnt[q.w - lo], 1u);
+        }
+        for (int j = max(body, head) + tid; j < s1; j += WG) {
+            const int id = a.hist_ids[j];
+            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], 1u);
         }
     }
     if (a.extra_a) {
@@ -570,7 +587,16 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
     constexpr int SEG = WG * EPT;
     constexpr int NV = EPT / 4;  // float4 per thread
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-    const int seg = blockIdx.x, row = blockIdx.y;
+    // Work item of this workgroup. Workgroups are dealt round-robin to the 8 XCDs (workgroup i on XCD i % 8);
+    // with xcd_map, XCD x takes a contiguous block of (row, segment) items, so a row's segments (and the reads
+    // of its history) mostly share one L2. Padding workgroups leave before any synchronization.
+    int item = blockIdx.x;
+    if (a.xcd_map) {
+        const int per = (a.n_rows * a.segs + 7) >> 3;
+        item = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    }
+    if (item >= a.n_rows * a.segs) return;
+    const int row = item / a.segs, seg = item - row * a.segs;
     const int lo = seg * SEG;
     const int hi = min(a.V, lo + SEG);
     const float* __restrict__ L = a.logits + (int64_t) row * a.row_stride;
@@ -642,13 +668,22 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
     } else {
         // ---- lower bound of the row's k-th value: each wave's ceil(k/4)-th largest lane maximum, smallest of
         // the four (at least 4*ceil(k/4) >= k logits of this segment reach it)
-        float m = v[0];
+        // (per lane: the largest and second largest logit; the wave bound is the larger of the k4-th largest lane
+        // maximum and the ceil(k4/2)-th largest second maximum, each reached by at least k4 logits; NaN counts
+        // as -inf here and never reaches a bound)
+        float m1 = -INFINITY, m2 = -INFINITY;
 #pragma unroll
-        for (int i = 1; i < EPT; ++i) m = fmaxf(m, v[i]);
-        const uint32_t sm = sort32_desc(ord_f32(m), lane);
+        for (int i = 0; i < EPT; ++i) {
+            const float x = v[i] == v[i] ? v[i] : -INFINITY;
+            m2 = fmaxf(m2, fminf(m1, x));
+            m1 = fmaxf(m1, x);
+        }
+        const uint32_t s1 = sort32_desc(ord_f32(m1), lane);
+        const uint32_t s2 = sort32_desc(ord_f32(m2), lane);
         const int k4 = (k + NW - 1) / NW;
-        const uint32_t qw = (uint32_t) __builtin_amdgcn_readlane((int) sm, k4 - 1);  // all lanes active
-        if (lane == 0) s_q[wave] = qw;
+        const uint32_t q1 = (uint32_t) __builtin_amdgcn_readlane((int) s1, k4 - 1);  // all lanes active
+        const uint32_t q2 = (uint32_t) __builtin_amdgcn_readlane((int) s2, (k4 + 1) / 2 - 1);
+        if (lane == 0) s_q[wave] = max(q1, q2);
         __syncthreads();
         const uint32_t q = min(min(s_q[0], s_q[1]), min(s_q[2], s_q[3]));
         const float t_f = fmaxf(floor32(q), floor64(t_row));
@@ -758,61 +793,6 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
     if (lane == 0) publish(a, row, tok);
 }
 
-// Grid (parts, rows): workgroup (p, r) counting-sorts the p-th slice of row r's raw history ids into buckets of
-// (1 << bucket_shift) ids in place of the same slice of part_ids, and records the slice's bucket offsets, so
-// that a sampling workgroup finds its segment's ids with two loads per part.
-__global__ __launch_bounds__(256) void partition_kernel(PartitionArgs a) {
-    __shared__ uint32_t s_cnt[MAX_BUCKETS];
-    __shared__ uint32_t s_wsum[4];
-    const int part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-    const int rs = max(a.hist_off[row], 0), re = min(a.hist_off[row + 1], a.cap);
-    const int len = max(re - rs, 0);
-    const int s = rs + (int) ((int64_t) len * part / a.parts);
-    const int e = rs + (int) ((int64_t) len * (part + 1) / a.parts);
-    for (int b = tid; b < MAX_BUCKETS; b += 256) s_cnt[b] = 0u;
-    __syncthreads();
-    for (int j = s + tid; j < e; j += 256) {
-        const int id = a.hist_ids[j];
-        if (id >= 0 && id < a.V) atomicAdd(&s_cnt[id >> a.bucket_shift], 1u);
-    }
-    __syncthreads();
-    // exclusive scan of the bucket counts: thread t owns buckets 4t .. 4t+3
-    uint32_t c[4], run = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        c[j] = s_cnt[4 * tid + j];
-        run += c[j];
-    }
-    uint32_t incl = run;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t y = (uint32_t) __builtin_amdgcn_ds_bpermute((lane - d) << 2, (int) incl);
-        if (lane >= d) incl += y;
-    }
-    if (lane == 63) s_wsum[wave] = incl;
-    __syncthreads();
-    uint32_t base = incl - run;
-    for (int w = 0; w < wave; ++w) base += s_wsum[w];
-    const uint32_t total = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
-    int32_t* bo = a.boff + ((int64_t) row * a.parts + part) * (a.n_buckets + 1);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int b = 4 * tid + j;
-        if (b < a.n_buckets) bo[b] = s + (int) base;
-        s_cnt[b] = base;  // becomes the bucket's write cursor
-        base += c[j];
-    }
-    if (tid == 0) bo[a.n_buckets] = s + (int) total;  // s + total <= e: only ids read from [s, e) are counted
-    __syncthreads();
-    for (int j = s + tid; j < e; j += 256) {
-        const int id = a.hist_ids[j];
-        if (id >= 0 && id < a.V) {
-            const uint32_t pos = atomicAdd(&s_cnt[id >> a.bucket_shift], 1u);
-            a.part_ids[s + (int) pos] = id;
-        }
-    }
-}
-
 __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
     const long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = expf_glibc(__uint_as_float(lo + (uint32_t) i));
@@ -820,7 +800,7 @@ __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
 
 template <bool G, bool P>
 hipError_t launch_ept(const RowsArgs& a, hipStream_t s) {
-    const dim3 grid(a.segs, a.n_rows), block(WG);
+    const dim3 grid(rows_grid(a)), block(WG);
     const size_t lds = P ? (size_t) a.seg_len * sizeof(uint32_t) : 0;
     switch (a.seg_len) {
         case 1024: hipLaunchKernelGGL((rows_kernel<G, P, 4>), grid, block, lds, s, a); break;
@@ -834,16 +814,15 @@ hipError_t launch_ept(const RowsArgs& a, hipStream_t s) {
 
 }  // namespace
 
+int rows_grid(const RowsArgs& a) {
+    const int w = a.n_rows * a.segs;
+    return a.xcd_map ? ((w + 7) & ~7) : w;
+}
+
 hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_t s) {
     if (a.p.k < 1 || a.p.k > KCAP) return hipErrorInvalidValue;
     if (greedy) return penalize ? launch_ept<true, true>(a, s) : launch_ept<true, false>(a, s);
     return penalize ? launch_ept<false, true>(a, s) : launch_ept<false, false>(a, s);
-}
-
-hipError_t launch_partition(const PartitionArgs& a, hipStream_t s) {
-    if (a.n_buckets > MAX_BUCKETS || a.parts < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(partition_kernel, dim3(a.parts, a.n_rows), dim3(256), 0, s, a);
-    return hipGetLastError();
 }
 
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s) {
