@@ -50,7 +50,7 @@ struct kls_sampler {
     int k = 0;
     int V = 0, max_rows = 0, device = 0;
     int bucket_shift = MIN_BUCKET_SHIFT, n_buckets = 0;
-    int seg_len_override = 0, target_wg = 300, share_min_wg = 1024, xcd_map = 1;
+    int seg_len_override = 0, target_wg = 300, wide_target_wg = 320, share_min_wg = 1024, xcd_map = 1;
     hipStream_t stream = nullptr;
 
     // token history: host copy (as the reference's counts_) + what has reached the device
@@ -60,6 +60,7 @@ struct kls_sampler {
     int32_t* d_hist_w = nullptr;    // [V] counts
     int32_t* d_hist_boff = nullptr; // [n_buckets + 1]
     int32_t* h_stage = nullptr;     // pinned staging for uploads: 2*V + n_buckets + 1
+    bool count_wide = false;        // a device count may reach 65536
 
     // scratch
     uint64_t* d_seg_cand = nullptr;
@@ -103,14 +104,22 @@ bool is_device_ptr(const void* p) {
     return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
-// Segment length: 256 threads x {4, 8, 16, 32} logits. The smallest length whose grid (rows x segments) stays
-// within the target workgroup count, so small batches spread over every CU and large ones keep long segments.
+// Segment length. Short segments (256 threads x {4, 8, 16, 32} logits): the smallest length whose grid (rows x
+// segments) stays within target_wg workgroups, so small batches spread over every CU. When even 8192 ids leave
+// too many workgroups, 1024-thread workgroups over 16384..65536 ids (one per CU), the smallest length within
+// wide_target_wg: every logit and the row's history are then read once per segment with the chip full.
 void segments_for(const kls_sampler* h, int rows, int* seg_len, int* segs) {
+    auto grid = [&](int sl) { return (long long) rows * ((h->V + sl - 1) / sl); };
     int sl = SEG_MIN;
-    if (h->seg_len_override >= SEG_MIN && h->seg_len_override <= SEG_MAX) {
-        sl = h->seg_len_override;
+    const int o = h->seg_len_override;
+    if (o >= SEG_MIN && o <= SEG_MAX && (o & (o - 1)) == 0) {
+        sl = o;
     } else {
-        while (sl < SEG_MAX && (long long) rows * ((h->V + sl - 1) / sl) > h->target_wg) sl *= 2;
+        while (sl < SEG_WIDE / 2 && grid(sl) > h->target_wg) sl *= 2;
+        if (grid(sl) > h->target_wg) {
+            sl = SEG_WIDE;
+            while (sl < SEG_MAX && grid(sl) > h->wide_target_wg) sl *= 2;
+        }
     }
     *seg_len = sl;
     *segs = (h->V + sl - 1) / sl;
@@ -125,9 +134,11 @@ int upload_history(kls_sampler* h, hipStream_t s) {
     int32_t* bo = h->h_stage + 2 * (size_t) h->V;
     const int n = (int) ent.size();
     int b = 0;
+    int32_t max_count = 0;
     for (int i = 0; i < n; ++i) {
         ids[i] = ent[i].first;
         w[i] = ent[i].second;
+        max_count = std::max(max_count, ent[i].second);
         const int bi = ent[i].first >> h->bucket_shift;
         while (b <= bi) bo[b++] = i;
     }
@@ -140,6 +151,8 @@ int upload_history(kls_sampler* h, hipStream_t s) {
     KLS_HIP(hipMemcpyAsync(h->d_hist_boff, bo, sizeof(int32_t) * (h->n_buckets + 1), hipMemcpyHostToDevice, s));
     KLS_HIP(hipStreamSynchronize(s));
     h->pending.clear();
+    // counts on the device add at most the pending ids and a step's drafts to the uploaded ones
+    h->count_wide = (int64_t) max_count + PENDING_CAP + VERIFY_MAX_ROWS >= 65536;
     return KLS_OK;
 }
 
@@ -173,6 +186,7 @@ RowsArgs step_args(kls_sampler* h, const float* logits, int rows, bool verify) {
         a.hist_ids = h->d_hist_ids;
         a.hist_w = h->d_hist_w;
         a.hist_boff = h->d_hist_boff;
+        a.count_wide = h->count_wide ? 1 : 0;
 
         a.extra_a = h->call_dev->pending;
         a.extra_a_n = &h->call_dev->n_pending;
@@ -342,6 +356,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     h->n_buckets = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;
     if (const char* e = getenv("KLS_SEG_LEN")) h->seg_len_override = atoi(e);
     if (const char* e = getenv("KLS_TARGET_WG")) h->target_wg = std::max(1, atoi(e));
+    if (const char* e = getenv("KLS_WIDE_TARGET_WG")) h->wide_target_wg = std::max(1, atoi(e));
     if (const char* e = getenv("KLS_SHARE_MIN_WG")) h->share_min_wg = atoi(e);
     if (const char* e = getenv("KLS_XCD_MAP")) h->xcd_map = atoi(e) != 0;
     (void) hipGetDevice(&h->device);
@@ -352,6 +367,10 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     };
     hipError_t e;
     if ((e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking)) != hipSuccess) return oom("stream", e);
+    if ((e = prepare_rows_kernels()) != hipSuccess) {
+        kls_destroy(h);
+        return fail(KLS_ERR_HIP, "kernel LDS limits", e);
+    }
     h->max_segs = (n_vocab + SEG_MIN - 1) / SEG_MIN;
     const size_t R = (size_t) max_rows;
 #define ALLOC(ptr, bytes) \

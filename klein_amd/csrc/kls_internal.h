@@ -12,10 +12,11 @@ constexpr int KCAP = 64;
 constexpr int VERIFY_MAX_ROWS = 16;
 // History ids accepted since the last device upload that ride along with a call.
 constexpr int PENDING_CAP = 256;
-// Segments (vocabulary ids per workgroup) are 256 threads x EPT elements, EPT in {4, 8, 16, 32}; with
-// penalties the segment's history counts live in LDS (4 B per id).
+// Segments (vocabulary ids per workgroup): 256 threads x EPT elements, EPT in {4, 8, 16, 32} (1024..8192 ids,
+// history counts in LDS at 4 B per id), or 1024 threads x {16, 32, 64} (16384..65536 ids, 2 B per id).
 constexpr int SEG_MIN = 1024;
-constexpr int SEG_MAX = 8192;
+constexpr int SEG_WIDE = 16384;  // first length served by 1024-thread workgroups
+constexpr int SEG_MAX = 65536;
 // History bucket width: history lists are partitioned into buckets of (1 << bucket_shift) ids, and segments
 // start on bucket boundaries so a workgroup finds its history slice with two loads.
 constexpr int MIN_BUCKET_SHIFT = 10;
@@ -52,7 +53,7 @@ struct RowsArgs {
     int32_t V;
     int32_t n_rows;
     int32_t segs;
-    int32_t seg_len;  // 256 * EPT
+    int32_t seg_len;  // ids per segment: workgroup threads x EPT
     int32_t xcd_map;  // 1: deal (row, segment) work so that a row's segments run on one XCD (see the kernel)
     SamplingParams p;
 
@@ -66,6 +67,7 @@ struct RowsArgs {
     const int32_t* hist_off;   // raw form: [n_rows + 1]
     int32_t bucket_shift;
     int32_t n_buckets;
+    int32_t count_wide;  // a history count may reach 65536 (16-bit count tables are then not used)
     // extra history ids counted on top: list A (count read from memory) for every row, list B's first
     // row*extra_b_step entries for row `row` (the verify step's drafts on the accepted path)
     const int32_t* extra_a;
@@ -94,6 +96,7 @@ struct RowsArgs {
 // Launchers (kls_kernels.hip). Return hipSuccess or the launch error.
 hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_t s);
 int rows_grid(const RowsArgs& a);  // workgroups launch_rows starts
+hipError_t prepare_rows_kernels();  // once per device: LDS limits of the kernels with large count tables
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s);
 
 }  // namespace kls

@@ -1,20 +1,21 @@
 // HIP kernels of the gfx950 token sampler.
 //
 // One fused kernel samples a batch of rows (klein src/sampler.cpp:17-89 per row, plus the verify accept rule of
-// src/engine.cpp:563-575 across rows). Grid = (segments, rows). A workgroup of 4 waves holds one segment of one
-// row (256 threads x EPT logits) in registers after a single coalesced HBM read:
+// src/engine.cpp:563-575 across rows). The grid is a list of (row, segment) work items; a workgroup of NW waves
+// (NW = 4 for short segments, 16 for long ones) holds one segment of one row (NW*64 threads x EPT logits) in
+// registers after a single coalesced HBM read:
 //   * penalties (sampler.cpp:18-29) are applied in-register by the one lane holding each id, from a count table
 //     of the segment's history ids staged in LDS; nothing is written to the logits or any global buffer;
 //   * greedy (sampler.cpp:31-39) keeps a per-lane (max, first id) and reduces across lanes and segments;
-//   * top-k (sampler.cpp:42-51): a lower bound of the row's k-th largest value is formed from the lane maxima
-//     (each wave's ceil(k/4)-th largest lane maximum; the smallest of the four, so at least k logits of the
-//     segment reach it) and from the best bound other workgroups of the row have published; one float compare
-//     per logit rejects nearly everything, and the few survivors are ordered by a 64-bit key (value
-//     descending, id ascending) with wave64 bitonic networks built from DPP and permlane swaps;
+//   * top-k (sampler.cpp:42-51): every lane contributes its two largest logits; the k-th largest of those
+//     (2 x NW*64 distinct logits) is a lower bound of the segment's k-th largest value, and with the best bound
+//     other workgroups of the row have published, one float compare per logit rejects nearly everything. The
+//     few survivors are ordered by a 64-bit key (value descending, id ascending) with wave64 bitonic networks
+//     built from DPP and permlane swaps;
 //   * the last workgroup of a row (ticket counter) merges the segment candidate lists into the row's sorted
 //     top-k and runs the O(k) tail on one wave: softmax with temperature (expf bit-identical to the host
-//     glibc's, sequential double sum), min-p, top-p and the draw (sampler.cpp:53-88);
-//   * in a verify step the last row to finish computes the accepted-prefix length.
+//     glibc's, double sums), min-p, top-p and the draw (sampler.cpp:53-88);
+//   * in a verify step each row publishes its token to pinned host memory; the host forms the accepted prefix.
 // Ticket counters and published bounds are reset by their last user, so launches replay from a captured graph
 // without memset nodes.
 #include "kls_internal.h"
@@ -22,20 +23,22 @@
 namespace kls {
 namespace {
 
-constexpr int WG = 256;
-constexpr int NW = WG / 64;
 constexpr int CW = 128;  // candidate slots per wave in LDS
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Workgroup memory of the sampling kernel, addressed directly (no generic pointers into LDS).
-extern __shared__ __align__(16) uint32_t s_cnt[];  // with penalties: the segment's history counts
-__shared__ uint64_t s_cand[NW][CW];                // per-wave candidate regions
-__shared__ uint64_t s_list[NW][64];                // per-wave sorted lists
-__shared__ uint64_t s_red[NW];
-__shared__ uint32_t s_q[NW];
-__shared__ int s_n[NW];
+// Workgroup memory of the sampling kernel, one set per workgroup width, addressed directly (no generic
+// pointers into LDS).
+extern __shared__ __align__(16) uint32_t s_cnt[];    // with penalties: the segment's history counts
+template <int NW> __shared__ uint64_t s_cand[NW][CW];  // per-wave candidate regions
+template <int NW> __shared__ uint64_t s_list[NW][64];  // per-wave sorted lists
+template <int NW> __shared__ uint64_t s_red[NW];
+template <int NW> __shared__ uint32_t s_q[NW];
+template <int NW> __shared__ int s_n[NW];
+template <int NW> __shared__ uint32_t s_mx[NW][64];    // per-wave sorted lane maxima
+template <int NW> __shared__ uint32_t s_mx4[4][64];    // their merges in groups of four waves
 __shared__ int s_last;
+
 
 // ---------------------------------------------------------------------------------------------------------
 // keys: order-preserving 32-bit image of the f32 value in the high word, ~id in the low word, so that a larger
@@ -168,33 +171,40 @@ __device__ __forceinline__ uint64_t merge64(uint64_t a, uint64_t b, int lane) {
     return bitonic_stage<64, true>(max64(a, b), lane);  // max of desc and asc is bitonic
 }
 
-template <int SIZE, int STRIDE>
+template <int SIZE, int STRIDE, bool DESC>
 __device__ __forceinline__ uint32_t bitonic_step32(uint32_t x, int lane) {
     const uint32_t y = (uint32_t) xor_lane<STRIDE>((int) x, lane);
-    const bool up = ((lane & SIZE) == 0);
+    const bool up = (((lane & SIZE) == 0) == DESC);
     const bool lower = (lane & STRIDE) == 0;
     return (lower == up) ? max(x, y) : min(x, y);
 }
 
-template <int SIZE>
+template <int SIZE, bool DESC>
 __device__ __forceinline__ uint32_t bitonic_stage32(uint32_t x, int lane) {
-    if constexpr (SIZE >= 64) x = bitonic_step32<SIZE, 32>(x, lane);
-    if constexpr (SIZE >= 32) x = bitonic_step32<SIZE, 16>(x, lane);
-    if constexpr (SIZE >= 16) x = bitonic_step32<SIZE, 8>(x, lane);
-    if constexpr (SIZE >= 8) x = bitonic_step32<SIZE, 4>(x, lane);
-    if constexpr (SIZE >= 4) x = bitonic_step32<SIZE, 2>(x, lane);
-    return bitonic_step32<SIZE, 1>(x, lane);
+    if constexpr (SIZE >= 64) x = bitonic_step32<SIZE, 32, DESC>(x, lane);
+    if constexpr (SIZE >= 32) x = bitonic_step32<SIZE, 16, DESC>(x, lane);
+    if constexpr (SIZE >= 16) x = bitonic_step32<SIZE, 8, DESC>(x, lane);
+    if constexpr (SIZE >= 8) x = bitonic_step32<SIZE, 4, DESC>(x, lane);
+    if constexpr (SIZE >= 4) x = bitonic_step32<SIZE, 2, DESC>(x, lane);
+    return bitonic_step32<SIZE, 1, DESC>(x, lane);
 }
 
-// Descending sort of one 32-bit value per lane.
-__device__ __forceinline__ uint32_t sort32_desc(uint32_t x, int lane) {
-    x = bitonic_stage32<2>(x, lane);
-    x = bitonic_stage32<4>(x, lane);
-    x = bitonic_stage32<8>(x, lane);
-    x = bitonic_stage32<16>(x, lane);
-    x = bitonic_stage32<32>(x, lane);
-    return bitonic_stage32<64>(x, lane);
+// Sorts one 32-bit value per lane across the wave (DESC: lane 0 holds the largest).
+template <bool DESC>
+__device__ __forceinline__ uint32_t sort32(uint32_t x, int lane) {
+    x = bitonic_stage32<2, DESC>(x, lane);
+    x = bitonic_stage32<4, DESC>(x, lane);
+    x = bitonic_stage32<8, DESC>(x, lane);
+    x = bitonic_stage32<16, DESC>(x, lane);
+    x = bitonic_stage32<32, DESC>(x, lane);
+    return bitonic_stage32<64, DESC>(x, lane);
 }
+
+// Top 64 of a descending list `a` and an ascending list `b`, descending.
+__device__ __forceinline__ uint32_t merge32(uint32_t a, uint32_t b, int lane) {
+    return bitonic_stage32<64, true>(max(a, b), lane);
+}
+
 
 __device__ __forceinline__ uint64_t wave_max64(uint64_t x, int lane) {
     x = max64(x, xor_lane64<32>(x, lane));
@@ -258,67 +268,125 @@ __device__ __forceinline__ float penalize(float l, uint32_t c, const SamplingPar
     return __fsub_rn(l, t);
 }
 
-// Counts the history ids that fall in [lo, hi) into the LDS table s_cnt[0 .. hi-lo).
-__device__ __forceinline__ void stage_history(const RowsArgs& a, int row, int lo, int hi) {
+// ---------------------------------------------------------------------------------------------------------
+// History counts in LDS. A table covers the ids [tlo, thi) of a segment. Entry i counts id tlo + i: a 32-bit
+// word each, or (C16) a 16-bit half of word i/2, bits 16*(i%2) up, which halves the table of a long segment.
+// 16-bit counts are exact while a row's history holds fewer than 65536 ids; longer histories take 32-bit
+// tables over half a segment at a time.
+
+// The 16-byte aligned body of the raw history prefetched ahead of the second half of the logits, per thread.
+constexpr int HR = 4;
+
+template <bool C16>
+__device__ __forceinline__ void cnt_add(int id, int tlo, int thi, uint32_t w) {
+    const uint32_t i = (uint32_t) id - (uint32_t) tlo;  // ids below tlo wrap to large values
+    if (i < (uint32_t) (thi - tlo)) {
+        if (C16)
+            atomicAdd(&s_cnt[i >> 1], w << ((i & 1u) << 4));
+        else
+            atomicAdd(&s_cnt[i], w);
+    }
+}
+
+template <int WG>
+__device__ __forceinline__ void cnt_zero(int words) {
+    const int n4 = (words + 3) & ~3;  // within the table: segments are multiples of 1024 ids
+    for (int i = 4 * (int) threadIdx.x; i < n4; i += 4 * WG) *reinterpret_cast<uint4*>(s_cnt + i) = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Where a row's raw history lies: ids [s0, s1) of hist_ids; [b0, b1) is its 16-byte aligned body (empty when the
+// array itself is not 16-byte aligned), of which each thread prefetched HR int4 starting at b0.
+struct RawHistory {
+    int s0 = 0, b0 = 0, b1 = 0, s1 = 0;
+};
+
+// Counts every history id in [tlo, thi) into the table: the prefetched int4s, the rest of a raw history, a
+// bucketed history, and the extra lists.
+// Without PREF the whole raw history is read from memory (hq unused).
+template <int WG, bool C16, bool PREF>
+__device__ __forceinline__ void count_history(const RowsArgs& a, int row, int tlo, int thi, const int4 (&hq)[HR],
+                                              const RawHistory& rh) {
     const int tid = threadIdx.x;
-    const int n4 = (hi - lo + 3) & ~3;  // <= seg_len: the table is zeroed in 16-byte stores
-    for (int i = 4 * tid; i < n4; i += 4 * WG) *reinterpret_cast<uint4*>(s_cnt + i) = make_uint4(0u, 0u, 0u, 0u);
-    __syncthreads();
-    if (a.hist_boff) {
-        // bucketed unique ids with counts: read the buckets that overlap [lo, hi)
-        const int b0 = lo >> a.bucket_shift;
-        const int b1 = min(a.n_buckets, (hi + (1 << a.bucket_shift) - 1) >> a.bucket_shift);
-        const int s0 = max(a.hist_boff[b0], 0), s1 = a.hist_boff[b1];
-        for (int j = s0 + tid; j < s1; j += WG) {
-            const int id = a.hist_ids[j];
-            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], (uint32_t) a.hist_w[j]);
+    if (a.hist_off) {
+        if (PREF) {
+#pragma unroll
+            for (int r = 0; r < HR; ++r) {
+                cnt_add<C16>(hq[r].x, tlo, thi, 1u);
+                cnt_add<C16>(hq[r].y, tlo, thi, 1u);
+                cnt_add<C16>(hq[r].z, tlo, thi, 1u);
+                cnt_add<C16>(hq[r].w, tlo, thi, 1u);
+            }
         }
-    } else if (a.hist_off) {
-        // raw ids of this row: every workgroup of the row scans them (from L2) and keeps those in its segment
-        const int s0 = max(a.hist_off[row], 0), s1 = a.hist_off[row + 1];
-        const int head = min(s1, (s0 + 3) & ~3), body = head + (max(s1 - head, 0) & ~3);
-        for (int j = s0 + tid; j < head; j += WG) {
-            const int id = a.hist_ids[j];
-            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], 1u);
-        }
-        for (int j = head + 4 * tid; j < body; j += 4 * WG) {
+        for (int j = rh.s0 + tid; j < rh.b0; j += WG) cnt_add<C16>(a.hist_ids[j], tlo, thi, 1u);
+        for (int j = rh.b0 + 4 * ((PREF ? HR * WG : 0) + tid); j < rh.b1; j += 4 * WG) {
             const int4 q = *reinterpret_cast<const int4*>(a.hist_ids + j);
-            if (q.x >= lo && q.x < hi) atomicAdd(&s_cnt[q.x - lo], 1u);
-            if (q.y >= lo && q.y < hi) atomicAdd(&s_cnt[q.y - lo], 1u);
-            if (q.z >= lo && q.z < hi) atomicAdd(&s_cnt[q.z - lo], 1u);
-            if (q.w >= lo && q.w < hi) atomicAdd(&s_cnt[q.w - lo], 1u);
+            cnt_add<C16>(q.x, tlo, thi, 1u);
+            cnt_add<C16>(q.y, tlo, thi, 1u);
+            cnt_add<C16>(q.z, tlo, thi, 1u);
+            cnt_add<C16>(q.w, tlo, thi, 1u);
         }
-        for (int j = max(body, head) + tid; j < s1; j += WG) {
-            const int id = a.hist_ids[j];
-            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], 1u);
-        }
+        for (int j = rh.b1 + tid; j < rh.s1; j += WG) cnt_add<C16>(a.hist_ids[j], tlo, thi, 1u);
+    } else if (a.hist_boff) {
+        // bucketed unique ids with counts: read the buckets that overlap [tlo, thi)
+        const int bb0 = tlo >> a.bucket_shift;
+        const int bb1 = min(a.n_buckets, (thi + (1 << a.bucket_shift) - 1) >> a.bucket_shift);
+        const int s0 = max(a.hist_boff[bb0], 0), s1 = a.hist_boff[bb1];
+        for (int j = s0 + tid; j < s1; j += WG) cnt_add<C16>(a.hist_ids[j], tlo, thi, (uint32_t) a.hist_w[j]);
     }
     if (a.extra_a) {
         const int na = min(max(*a.extra_a_n, 0), PENDING_CAP);
-        for (int j = tid; j < na; j += WG) {
-            const int id = a.extra_a[j];
-            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], 1u);
-        }
+        for (int j = tid; j < na; j += WG) cnt_add<C16>(a.extra_a[j], tlo, thi, 1u);
     }
     if (a.extra_b) {
         const int nb = min(row * a.extra_b_step, VERIFY_MAX_ROWS);
-        for (int j = tid; j < nb; j += WG) {
-            const int id = a.extra_b[j];
-            if (id >= lo && id < hi) atomicAdd(&s_cnt[id - lo], 1u);
+        for (int j = tid; j < nb; j += WG) cnt_add<C16>(a.extra_b[j], tlo, thi, 1u);
+    }
+}
+
+// Applies the table's counts to the logits this thread holds in groups I0 <= i < I1 (ids lo + 4*(i*WG + tid) + e).
+template <int WG, int EPT, bool C16, int I0, int I1>
+__device__ __forceinline__ void apply_counts(float (&v)[EPT], int lo, int hi, int tlo, const SamplingParams& p) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+        const int id0 = lo + 4 * (i * WG + tid);
+        if (id0 >= hi) continue;
+        const int t = id0 - tlo;  // a multiple of 4
+        uint32_t c[4];
+        if (C16) {
+            const uint2 q = *reinterpret_cast<const uint2*>(s_cnt + (t >> 1));
+            c[0] = q.x & 0xffffu;
+            c[1] = q.x >> 16;
+            c[2] = q.y & 0xffffu;
+            c[3] = q.y >> 16;
+        } else {
+            const uint4 q = *reinterpret_cast<const uint4*>(s_cnt + t);
+            c[0] = q.x;
+            c[1] = q.y;
+            c[2] = q.z;
+            c[3] = q.w;
+        }
+#pragma unroll
+        for (int e = 1; e < 4; ++e)
+            if (id0 + e >= hi) c[e] = 0u;
+        if ((c[0] | c[1] | c[2] | c[3]) != 0u) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (c[e] != 0u) v[4 * i + e] = penalize(v[4 * i + e], c[e], p);
         }
     }
-    __syncthreads();
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Candidate lists. Fast path: survivors of the filter are appended to the wave's LDS region and, when the four
-// regions together hold at most 64 keys, sorted once. Larger sets are folded chunk by chunk (sort + bitonic
-// merge). The fold lives out of line: it is the only large network, and the streaming loops stay small.
+// Candidate lists. Survivors of the filter are appended to the wave's LDS region. The workgroup's regions are
+// then read as one list in chunks of 64: one chunk is sorted once; more are sorted by one wave each and merged.
+// Regions that fill up are folded (sort + bitonic merge) on the slow paths only.
 
 // Descending top-64 of `lst` (descending; ignored when !have) and the n keys of the wave's region.
+template <int NW>
 __device__ __forceinline__ uint64_t fold_region(int wave, int n, uint64_t lst, bool have, int lane) {
     for (int c0 = 0; c0 < n; c0 += 64) {
-        const uint64_t key = (c0 + lane < n) ? s_cand[wave][c0 + lane] : 0ull;
+        const uint64_t key = (c0 + lane < n) ? s_cand<NW>[wave][c0 + lane] : 0ull;
         if (!have) {
             lst = sort64<true>(key, lane);
             have = true;
@@ -329,11 +397,8 @@ __device__ __forceinline__ uint64_t fold_region(int wave, int n, uint64_t lst, b
     return have ? lst : 0ull;
 }
 
-__device__ __forceinline__ uint64_t sort_desc(uint64_t key, int lane) { return sort64<true>(key, lane); }
-
-__device__ __forceinline__ uint64_t merge_desc_asc(uint64_t a, uint64_t b, int lane) { return merge64(a, b, lane); }
-
 // Appends the keys of `pass` lanes to the wave's region; records an overflow instead of folding.
+template <int NW>
 struct WaveCollect {
     int n = 0;
     bool overflow = false;
@@ -345,12 +410,13 @@ struct WaveCollect {
             overflow = true;
             return;
         }
-        if (pass) s_cand[wave][n + mbcnt(m)] = key;
+        if (pass) s_cand<NW>[wave][n + mbcnt(m)] = key;
         n += c;
     }
 };
 
 // A wave's descending top-64 over a stream of offers, folding its region whenever it fills (slow paths).
+template <int NW>
 struct WaveTopK {
     uint64_t lst = 0ull;
     bool have = false;
@@ -362,99 +428,146 @@ struct WaveTopK {
         const int c = __popcll(m);
         if (n + c > CW) {
             __builtin_amdgcn_wave_barrier();
-            lst = fold_region(wave, n, lst, have, lane);
+            lst = fold_region<NW>(wave, n, lst, have, lane);
             have = true;
             n = 0;
             own = rdlane64(lst, k - 1);
             __builtin_amdgcn_wave_barrier();
         }
-        if (pass) s_cand[wave][n + mbcnt(m)] = key;
+        if (pass) s_cand<NW>[wave][n + mbcnt(m)] = key;
         n += c;
     }
     __device__ __forceinline__ uint64_t finish(int wave, int lane) {
         __builtin_amdgcn_wave_barrier();
-        return fold_region(wave, n, lst, have, lane);
+        return fold_region<NW>(wave, n, lst, have, lane);
     }
 };
 
-// The workgroup's descending top-64 of what its waves collected, in wave 0 (other waves get 0); keys below
-// `floor_key` are dropped. Returns false (in every thread) if a region overflowed.
-__device__ __forceinline__ bool wg_select(const WaveCollect& w, uint64_t floor_key, int lane, int wave, uint64_t* out) {
-    if (lane == 0) s_n[wave] = w.overflow ? -1 : w.n;
+// Wave 0's descending top-64 of the lists in s_list[0..n) (other waves return 0).
+template <int NW>
+__device__ __forceinline__ uint64_t merge_lists(int n, int lane, int wave) {
+    if (wave != 0) return 0ull;
+    uint64_t lst = s_list<NW>[0][lane];
+    for (int o = 1; o < n; ++o) lst = merge64(lst, s_list<NW>[o][63 - lane], lane);
+    return lst;
+}
+
+// The workgroup's descending top-64 of what its waves collected, in wave 0 (other waves get 0). Returns false
+// (in every thread) if a region overflowed.
+template <int NW>
+__device__ __forceinline__ bool wg_select(const WaveCollect<NW>& w, int lane, int wave, uint64_t* out) {
+    if (lane == 0) s_n<NW>[wave] = w.overflow ? -1 : w.n;
     __syncthreads();
-    const int n0 = s_n[0], n1 = s_n[1], n2 = s_n[2], n3 = s_n[3];
+    int cnt[NW];
+    int total = 0;
+    bool bad = false;
+#pragma unroll
+    for (int r = 0; r < NW; ++r) {
+        cnt[r] = s_n<NW>[r];
+        bad |= cnt[r] < 0;
+        total += cnt[r];
+    }
     *out = 0ull;
-    if ((n0 | n1 | n2 | n3) < 0) return false;
-    if (n0 + n1 + n2 + n3 <= 64) {
-        if (wave == 0) {
-            uint64_t key = 0ull;
-            if (lane < n0)
-                key = s_cand[0][lane];
-            else if (lane < n0 + n1)
-                key = s_cand[1][lane - n0];
-            else if (lane < n0 + n1 + n2)
-                key = s_cand[2][lane - n0 - n1];
-            else if (lane < n0 + n1 + n2 + n3)
-                key = s_cand[3][lane - n0 - n1 - n2];
-            *out = sort_desc(key < floor_key ? 0ull : key, lane);
-        }
+    if (bad) return false;
+    const int nc = (total + 63) >> 6;
+    if (nc > NW) {
+        // more chunks than waves: every wave folds its own region, wave 0 merges the lists
+        const uint64_t lst = fold_region<NW>(wave, s_n<NW>[wave], 0ull, false, lane);
+        s_list<NW>[wave][lane] = lst;
+        __syncthreads();
+        *out = merge_lists<NW>(NW, lane, wave);
         return true;
     }
-    uint64_t lst = fold_region(wave, s_n[wave], 0ull, false, lane);
-    s_list[wave][lane] = lst >= floor_key ? lst : 0ull;
-    __syncthreads();
-    if (wave == 0) {
-        lst = s_list[0][lane];
+    uint64_t lst = 0ull;
+    if (wave < nc) {
+        // chunk `wave` of the concatenated regions
+        const int j = 64 * wave + lane;
+        uint64_t key = 0ull;
+        int base = 0;
 #pragma unroll
-        for (int o = 1; o < NW; ++o) lst = merge_desc_asc(lst, s_list[o][63 - lane], lane);
-        *out = lst;
+        for (int r = 0; r < NW; ++r) {
+            if (j >= base && j < base + cnt[r]) key = s_cand<NW>[r][j - base];
+            base += cnt[r];
+        }
+        lst = sort64<true>(key, lane);
     }
+    if (nc <= 1) {
+        *out = wave == 0 ? lst : 0ull;
+        return true;
+    }
+    if (wave < nc) s_list<NW>[wave][lane] = lst;
+    __syncthreads();
+    *out = merge_lists<NW>(nc, lane, wave);
     return true;
 }
 
-// Slow path of a segment (a region overflowed, e.g. many logits equal to the bound): re-read the segment and
-// keep exact per-wave lists with folding, then merge. Returns the top-64 in wave 0.
-__device__ __forceinline__ uint64_t segment_slow(const RowsArgs& a, const float* __restrict__ L, int lo, int hi, bool pen,
-                                                 uint64_t t_row, int lane, int wave) {
-    const int k = a.p.k;
-    WaveTopK w;
-    for (int base = lo + 4 * (wave * 64 + lane); base - 4 * lane < hi; base += 4 * WG) {
+// Scans ids [slo, shi) into the waves' exact lists (slow path), with penalties from the table over [tlo, ...).
+template <int NW, bool C16>
+__device__ __forceinline__ void scan_exact(WaveTopK<NW>& w, const RowsArgs& a, const float* __restrict__ L, int slo,
+                                           int shi, bool pen, int tlo, uint64_t t_row, int lane, int wave) {
+    constexpr int WG = NW * 64;
+    for (int base = slo + 4 * (wave * 64 + lane); base - 4 * lane < shi; base += 4 * WG) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int id = base + e;
             float x = __uint_as_float(0x7fc00000u);
-            if (id < hi) {
+            if (id < shi) {
                 x = L[id];
-                if (pen && s_cnt[id - lo] != 0u) x = penalize(x, s_cnt[id - lo], a.p);
+                if (pen) {
+                    const uint32_t i = (uint32_t) (id - tlo);
+                    const uint32_t c = C16 ? (s_cnt[i >> 1] >> ((i & 1u) << 4)) & 0xffffu : s_cnt[i];
+                    if (c != 0u) x = penalize(x, c, a.p);
+                }
             }
             const uint64_t key = x == x ? mk_key(x, id) : 0ull;
-            w.offer(wave, key != 0ull && key > max64(t_row, w.own), key, k, lane);
+            w.offer(wave, key != 0ull && key > max64(t_row, w.own), key, a.p.k, lane);
         }
     }
-    uint64_t lst = w.finish(wave, lane);
-    s_list[wave][lane] = lst;
+}
+
+// Slow path of a segment (a region overflowed, e.g. many logits equal to the bound): re-read the segment and
+// keep exact per-wave lists with folding, then merge. With `wide` counts the history is staged again, half a
+// segment at a time. Returns the top-64 in wave 0.
+template <int NW, int SEG, bool C16>
+__device__ __forceinline__ uint64_t segment_slow(const RowsArgs& a, const float* __restrict__ L, int row, int lo, int hi,
+                                                 bool pen, bool wide, const RawHistory& rh, uint64_t t_row, int lane,
+                                                 int wave) {
+    constexpr int WG = NW * 64;
+    WaveTopK<NW> w;
+    if (!pen || !wide) {
+        scan_exact<NW, C16>(w, a, L, lo, hi, pen, lo, t_row, lane, wave);
+    } else {
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) {
+            const int wlo = lo + h * (SEG / 2), whi = min(hi, wlo + SEG / 2);
+            if (wlo >= hi) break;
+            __syncthreads();
+            cnt_zero<WG>(whi - wlo);
+            __syncthreads();
+            const int4 none[HR] = {};
+            count_history<WG, false, false>(a, row, wlo, whi, none, rh);
+            __syncthreads();
+            scan_exact<NW, false>(w, a, L, wlo, whi, true, wlo, t_row, lane, wave);
+        }
+    }
+    s_list<NW>[wave][lane] = w.finish(wave, lane);
     __syncthreads();
-    if (wave != 0) return 0ull;
-    lst = s_list[0][lane];
-    for (int o = 1; o < NW; ++o) lst = merge_desc_asc(lst, s_list[o][63 - lane], lane);
-    return lst;
+    return merge_lists<NW>(NW, lane, wave);
 }
 
 // Slow path of the row merge: every segment list entry at or above `ts`, folded exactly.
+template <int NW>
 __device__ __forceinline__ uint64_t merge_slow(const uint64_t* cand, int segs, int k, uint64_t ts, int lane, int wave) {
-    WaveTopK w;
+    WaveTopK<NW> w;
     for (int s = wave; s < segs; s += NW) {
         const uint64_t key = lane < k ? load_dev(&cand[(int64_t) s * KCAP + lane]) : 0ull;
         w.offer(wave, key != 0ull && key >= ts && key > w.own, key, k, lane);
     }
-    uint64_t lst = w.finish(wave, lane);
-    s_list[wave][lane] = lst;
+    s_list<NW>[wave][lane] = w.finish(wave, lane);
     __syncthreads();
-    if (wave != 0) return 0ull;
-    lst = s_list[0][lane];
-    for (int o = 1; o < NW; ++o) lst = merge_desc_asc(lst, s_list[o][63 - lane], lane);
-    return lst;
+    return merge_lists<NW>(NW, lane, wave);
 }
+
 
 // ---------------------------------------------------------------------------------------------------------
 // The O(k) tail of src/sampler.cpp:53-88 on one wave: lane i holds the i-th candidate (value descending, id
@@ -527,7 +640,7 @@ __device__ __forceinline__ double chain_draw(double r, float p, int n, int lane)
     return mine;
 }
 
-__device__ int sample_tail(uint64_t lst, int kk, const SamplingParams& p, double u, int lane, float* dbg_probs,
+__device__ int sample_tail(uint64_t lst, int kk, const SamplingParams p, double u, int lane, float* dbg_probs,
                            int32_t* dbg_meta) {
     if (kk == 0) return 0;
     const bool act = lane < kk;
@@ -582,10 +695,15 @@ __device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok) {
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-template <bool GREEDY, bool PENALIZE, int EPT>
-__global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
+template <bool GREEDY, bool PENALIZE, int NW, int EPT>
+__global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
+    constexpr int WG = NW * 64;
     constexpr int SEG = WG * EPT;
-    constexpr int NV = EPT / 4;  // float4 per thread
+    constexpr int NV = EPT / 4;    // float4 per thread
+    constexpr int NVH = NV / 2;    // float4 loaded before the history prefetch
+    constexpr bool C16 = NW > 4;   // 16-bit history counts (segments of 16384 ids and more)
+    static_assert(NW == 4 || NW == 16, "workgroup width");
+    static_assert(!C16 || NV % 2 == 0, "half-segment windows");
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     // Work item of this workgroup. Workgroups are dealt round-robin to the 8 XCDs (workgroup i on XCD i % 8);
     // with xcd_map, XCD x takes a contiguous block of (row, segment) items, so a row's segments (and the reads
@@ -607,10 +725,35 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
     const uint64_t t_row =
         a.share_bounds ? __hip_atomic_load(&a.row_thr[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
 
-    // ---- one coalesced read of the segment: thread t holds ids lo + 4*(i*256 + t) + e
+    // ---- one coalesced read of the segment: thread t holds ids lo + 4*(i*WG + t) + e. The first half is
+    // issued before anything that waits on memory; the row's raw history (a prefetch into registers) goes
+    // between the halves, so its counts are staged while the second half is in flight.
     float v[EPT];
+    int4 hq[HR];
+#pragma unroll
+    for (int r = 0; r < HR; ++r) hq[r] = make_int4(-1, -1, -1, -1);
+    RawHistory rh;
+    bool wide = false;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
+        if (PENALIZE && i == NVH) {
+            if (a.hist_off) {
+                rh.s0 = max(a.hist_off[row], 0);
+                rh.s1 = max(a.hist_off[row + 1], rh.s0);
+                const bool hv = (reinterpret_cast<uintptr_t>(a.hist_ids) & 15u) == 0;
+                rh.b0 = hv ? min(rh.s1, (rh.s0 + 3) & ~3) : rh.s1;
+                rh.b1 = hv ? max(rh.b0, rh.s1 & ~3) : rh.s1;
+#pragma unroll
+                for (int r = 0; r < HR; ++r) {
+                    const int j = rh.b0 + 4 * (r * WG + tid);
+                    if (j < rh.b1) hq[r] = *reinterpret_cast<const int4*>(a.hist_ids + j);
+                }
+            }
+            // counts reach 65536 only with that many history ids in the row (extras included)
+            const int extra = (a.extra_a ? PENDING_CAP : 0) + (a.extra_b ? VERIFY_MAX_ROWS : 0);
+            wide = C16 && (a.count_wide != 0 || (rh.s1 - rh.s0) + extra >= 65536);
+            if (!wide) cnt_zero<WG>(C16 ? (hi - lo + 1) / 2 : hi - lo);
+        }
         const int base = lo + 4 * (i * WG + tid);
         if (vec && base + 3 < hi) {
             const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(L + base));
@@ -624,26 +767,26 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
         }
     }
     if (PENALIZE) {
-        stage_history(a, row, lo, hi);
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int off = 4 * (i * WG + tid);
-            if (lo + off >= hi) continue;
-            uint32_t c[4];
-            if (lo + off + 3 < hi) {
-                const uint4 q = *reinterpret_cast<const uint4*>(s_cnt + off);
-                c[0] = q.x;
-                c[1] = q.y;
-                c[2] = q.z;
-                c[3] = q.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) c[e] = (lo + off + e < hi) ? s_cnt[off + e] : 0u;
-            }
-            if ((c[0] | c[1] | c[2] | c[3]) != 0u) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (c[e] != 0u) v[4 * i + e] = penalize(v[4 * i + e], c[e], a.p);
+        if (!wide) {
+            __syncthreads();  // table zeroed
+            count_history<WG, C16, true>(a, row, lo, hi, hq, rh);
+            __syncthreads();
+            apply_counts<WG, EPT, C16, 0, NV>(v, lo, hi, lo, a.p);
+        } else if constexpr (C16) {
+            // 32-bit counts over half a segment at a time
+            const int mid = min(hi, lo + SEG / 2);
+            cnt_zero<WG>(mid - lo);
+            __syncthreads();
+            count_history<WG, false, true>(a, row, lo, mid, hq, rh);
+            __syncthreads();
+            apply_counts<WG, EPT, false, 0, NV / 2>(v, lo, hi, lo, a.p);
+            if (mid < hi) {
+                __syncthreads();
+                cnt_zero<WG>(hi - mid);
+                __syncthreads();
+                count_history<WG, false, true>(a, row, mid, hi, hq, rh);
+                __syncthreads();
+                apply_counts<WG, EPT, false, NV / 2, NV>(v, lo, hi, mid, a.p);
             }
         }
     }
@@ -662,15 +805,19 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
                 }
         uint64_t key = best_v > -INFINITY ? mk_key(best_v, best_id) : 0ull;
         key = wave_max64(key, lane);
-        if (lane == 0) s_red[wave] = key;
+        if (lane == 0) s_red<NW>[wave] = key;
         __syncthreads();
-        if (tid == 0) store_dev(&seg_out[0], max64(max64(s_red[0], s_red[1]), max64(s_red[2], s_red[3])));
+        if (tid == 0) {
+            uint64_t m = s_red<NW>[0];
+#pragma unroll
+            for (int o = 1; o < NW; ++o) m = max64(m, s_red<NW>[o]);
+            store_dev(&seg_out[0], m);
+        }
     } else {
-        // ---- lower bound of the row's k-th value: each wave's ceil(k/4)-th largest lane maximum, smallest of
-        // the four (at least 4*ceil(k/4) >= k logits of this segment reach it)
-        // (per lane: the largest and second largest logit; the wave bound is the larger of the k4-th largest lane
-        // maximum and the ceil(k4/2)-th largest second maximum, each reached by at least k4 logits; NaN counts
-        // as -inf here and never reaches a bound)
+        // ---- lower bound of the segment's k-th value: every lane contributes its largest and second largest
+        // logit (NaN counts as -inf and never reaches a bound); the k-th largest of these 2*WG distinct logits is
+        // reached by at least k logits of the segment. Each wave sorts its lane values and keeps its top 64,
+        // and the waves' lists are merged (in groups of four for 16 waves).
         float m1 = -INFINITY, m2 = -INFINITY;
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
@@ -678,18 +825,32 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
             m2 = fmaxf(m2, fminf(m1, x));
             m1 = fmaxf(m1, x);
         }
-        const uint32_t s1 = sort32_desc(ord_f32(m1), lane);
-        const uint32_t s2 = sort32_desc(ord_f32(m2), lane);
-        const int k4 = (k + NW - 1) / NW;
-        const uint32_t q1 = (uint32_t) __builtin_amdgcn_readlane((int) s1, k4 - 1);  // all lanes active
-        const uint32_t q2 = (uint32_t) __builtin_amdgcn_readlane((int) s2, (k4 + 1) / 2 - 1);
-        if (lane == 0) s_q[wave] = max(q1, q2);
+        const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
+        const uint32_t l2 = sort32<false>(ord_f32(m2), lane);
+        s_mx<NW>[wave][lane] = bitonic_stage32<64, true>(max(l1, l2), lane);
         __syncthreads();
-        const uint32_t q = min(min(s_q[0], s_q[1]), min(s_q[2], s_q[3]));
+        uint32_t gl;
+        if constexpr (NW == 4) {
+            gl = s_mx<NW>[0][lane];
+#pragma unroll
+            for (int o = 1; o < NW; ++o) gl = merge32(gl, s_mx<NW>[o][63 - lane], lane);
+        } else {
+            if (wave < 4) {
+                gl = s_mx<NW>[4 * wave][lane];
+#pragma unroll
+                for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx<NW>[4 * wave + o][63 - lane], lane);
+                s_mx4<NW>[wave][lane] = gl;
+            }
+            __syncthreads();
+            gl = s_mx4<NW>[0][lane];
+#pragma unroll
+            for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx4<NW>[o][63 - lane], lane);
+        }
+        const uint32_t q = (uint32_t) rdlanei((int) gl, k - 1);  // all lanes active
         const float t_f = fmaxf(floor32(q), floor64(t_row));
 
         // ---- filter: one compare per logit; survivors go to the wave's LDS region
-        WaveCollect w;
+        WaveCollect<NW> w;
 #pragma unroll
         for (int i = 0; i < NV; ++i)
 #pragma unroll
@@ -702,7 +863,8 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
                 }
             }
         uint64_t lst;
-        if (!wg_select(w, 0ull, lane, wave, &lst)) lst = segment_slow(a, L, lo, hi, PENALIZE, t_row, lane, wave);
+        if (!wg_select<NW>(w, lane, wave, &lst))
+            lst = segment_slow<NW, SEG, C16>(a, L, row, lo, hi, PENALIZE, wide, rh, t_row, lane, wave);
         if (wave == 0) {
             if (lane < k) store_dev(&seg_out[lane], lst);
             if (a.share_bounds) {
@@ -730,10 +892,11 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
         uint64_t m = 0ull;
         for (int s = tid; s < a.segs; s += WG) m = max64(m, load_dev(&cand[(int64_t) s * KCAP]));
         m = wave_max64(m, lane);
-        if (lane == 0) s_red[wave] = m;
+        if (lane == 0) s_red<NW>[wave] = m;
         __syncthreads();
         if (tid != 0) return;
-        m = max64(max64(s_red[0], s_red[1]), max64(s_red[2], s_red[3]));
+#pragma unroll
+        for (int o = 0; o < NW; ++o) m = max64(m, s_red<NW>[o]);
         if (a.dbg_meta) {
             a.dbg_meta[row * 2] = 0;
             a.dbg_meta[row * 2 + 1] = 0;
@@ -744,9 +907,9 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
 
     // Lower bound of the row's k-th value from the heads of the segment lists: H = the first J = ceil(k/segs)
     // entries of every list (J*segs >= k distinct logits). With |H| <= 64 the bound is the k-th largest value in H;
-    // otherwise H is dealt round-robin to the four waves and the bound is the smallest of the waves'
-    // ceil(k/4)-th largest values. Either way at least k logits reach it, so the row's top-k are among the list
-    // entries at or above it. Up to 64 lists stay in registers (16 per wave) while the bound is formed.
+    // otherwise H is dealt round-robin to the waves and the bound is the smallest of the waves'
+    // ceil(k/NW)-th largest values. Either way at least k logits reach it, so the row's top-k are among the list
+    // entries at or above it. Up to 16*NW lists stay in registers (16 per wave) while the bound is formed.
     constexpr int RB = 16;
     const int J = (k + a.segs - 1) / a.segs;
     const int nH = min(a.segs * J, WG);
@@ -760,12 +923,15 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
         const int s = wave + NW * r;
         key[r] = (inreg && s < a.segs && lane < k) ? load_dev(&cand[(int64_t) s * KCAP + lane]) : 0ull;
     }
-    const uint32_t sv = sort32_desc((uint32_t) (hv >> 32), lane);
+    const uint32_t sv = sort32<true>((uint32_t) (hv >> 32), lane);
     const uint32_t qw = (uint32_t) rdlanei((int) sv, (one ? k : (k + NW - 1) / NW) - 1);  // all lanes active
-    if (lane == 0) s_q[wave] = (one && wave != 0) ? 0xffffffffu : qw;
+    if (lane == 0) s_q<NW>[wave] = (one && wave != 0) ? 0xffffffffu : qw;
     __syncthreads();
-    const uint64_t ts = (uint64_t) min(min(s_q[0], s_q[1]), min(s_q[2], s_q[3])) << 32;
-    WaveCollect w;
+    uint32_t qm = s_q<NW>[0];
+#pragma unroll
+    for (int o = 1; o < NW; ++o) qm = min(qm, s_q<NW>[o]);
+    const uint64_t ts = (uint64_t) qm << 32;
+    WaveCollect<NW> w;
     if (inreg) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) w.offer(wave, key[r] != 0ull && key[r] >= ts, key[r]);
@@ -781,9 +947,9 @@ __global__ __launch_bounds__(WG) void rows_kernel(RowsArgs a) {
         }
     }
     uint64_t lst;
-    if (!wg_select(w, 0ull, lane, wave, &lst)) {
+    if (!wg_select<NW>(w, lane, wave, &lst)) {
         __syncthreads();
-        lst = merge_slow(cand, a.segs, k, ts, lane, wave);
+        lst = merge_slow<NW>(cand, a.segs, k, ts, lane, wave);
     }
     if (wave != 0) return;
     const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
@@ -798,18 +964,39 @@ __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
     if (i < n) out[i] = expf_glibc(__uint_as_float(lo + (uint32_t) i));
 }
 
+// LDS of the history count table: 4 bytes per id for 4-wave workgroups, 2 for 16-wave ones.
+template <bool P, int NW, int EPT>
+constexpr size_t table_bytes() {
+    return P ? (size_t) NW * 64 * EPT * (NW > 4 ? 2 : 4) : 0;
+}
+
+template <bool G, bool P, int NW, int EPT>
+hipError_t launch_cfg(const RowsArgs& a, hipStream_t s) {
+    constexpr size_t lds = table_bytes<P, NW, EPT>();
+    hipLaunchKernelGGL((rows_kernel<G, P, NW, EPT>), dim3(rows_grid(a)), dim3(NW * 64), lds, s, a);
+    return hipGetLastError();
+}
+
 template <bool G, bool P>
-hipError_t launch_ept(const RowsArgs& a, hipStream_t s) {
-    const dim3 grid(rows_grid(a)), block(WG);
-    const size_t lds = P ? (size_t) a.seg_len * sizeof(uint32_t) : 0;
+hipError_t launch_gp(const RowsArgs& a, hipStream_t s) {
     switch (a.seg_len) {
-        case 1024: hipLaunchKernelGGL((rows_kernel<G, P, 4>), grid, block, lds, s, a); break;
-        case 2048: hipLaunchKernelGGL((rows_kernel<G, P, 8>), grid, block, lds, s, a); break;
-        case 4096: hipLaunchKernelGGL((rows_kernel<G, P, 16>), grid, block, lds, s, a); break;
-        case 8192: hipLaunchKernelGGL((rows_kernel<G, P, 32>), grid, block, lds, s, a); break;
+        case 1024: return launch_cfg<G, P, 4, 4>(a, s);
+        case 2048: return launch_cfg<G, P, 4, 8>(a, s);
+        case 4096: return launch_cfg<G, P, 4, 16>(a, s);
+        case 8192: return launch_cfg<G, P, 4, 32>(a, s);
+        case 16384: return launch_cfg<G, P, 16, 16>(a, s);
+        case 32768: return launch_cfg<G, P, 16, 32>(a, s);
+        case 65536: return launch_cfg<G, P, 16, 64>(a, s);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+}
+
+template <bool G, bool P, int NW, int EPT>
+hipError_t allow_lds() {
+    constexpr size_t b = table_bytes<P, NW, EPT>();
+    if (b <= 65536) return hipSuccess;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&rows_kernel<G, P, NW, EPT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int) b);
 }
 
 }  // namespace
@@ -819,10 +1006,16 @@ int rows_grid(const RowsArgs& a) {
     return a.xcd_map ? ((w + 7) & ~7) : w;
 }
 
+hipError_t prepare_rows_kernels() {
+    hipError_t e = allow_lds<false, true, 16, 64>();
+    if (e == hipSuccess) e = allow_lds<true, true, 16, 64>();
+    return e;
+}
+
 hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_t s) {
     if (a.p.k < 1 || a.p.k > KCAP) return hipErrorInvalidValue;
-    if (greedy) return penalize ? launch_ept<true, true>(a, s) : launch_ept<true, false>(a, s);
-    return penalize ? launch_ept<false, true>(a, s) : launch_ept<false, false>(a, s);
+    if (greedy) return penalize ? launch_gp<true, true>(a, s) : launch_gp<true, false>(a, s);
+    return penalize ? launch_gp<false, true>(a, s) : launch_gp<false, false>(a, s);
 }
 
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s) {
