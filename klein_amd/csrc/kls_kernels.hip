@@ -26,6 +26,10 @@ namespace {
 constexpr int CW = 128;  // candidate slots per wave in LDS
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Buffer resource word 3 for raw (stride 0) 32-bit data on gfx9-family parts, and the non-temporal load policy.
+constexpr int kRawBufferFlags = 0x00020000;
+constexpr int kNonTemporal = 2;
 
 // Workgroup memory of the sampling kernel, one set per workgroup width, addressed directly (no generic
 // pointers into LDS).
@@ -260,9 +264,11 @@ __device__ __forceinline__ float expf_glibc(float x) {
 }
 
 // Penalty of src/sampler.cpp:24-25 for an id seen `c` > 0 times: repetition first, then
-// l - (presence + frequency * (float)c), each operation rounded separately (no contraction).
+// l - (presence + frequency * (float)c), each operation rounded separately (no contraction). Branch-free: with a
+// repetition penalty of 1 both l/1 and l*1 are l, as the reference's skipped step leaves it.
 __device__ __forceinline__ float penalize(float l, uint32_t c, const SamplingParams& p) {
-    if (p.repetition != 1.0f) l = l > 0.0f ? __fdiv_rn(l, p.repetition) : __fmul_rn(l, p.repetition);
+    const float d = __fdiv_rn(l, p.repetition), m = __fmul_rn(l, p.repetition);
+    l = l > 0.0f ? d : m;
     const float f = __fmul_rn(p.frequency, __uint2float_rn(c));
     const float t = __fadd_rn(p.presence, f);
     return __fsub_rn(l, t);
@@ -343,38 +349,41 @@ __device__ __forceinline__ void count_history(const RowsArgs& a, int row, int tl
     }
 }
 
-// Applies the table's counts to the logits this thread holds in groups I0 <= i < I1 (ids lo + 4*(i*WG + tid) + e).
-template <int WG, int EPT, bool C16, int I0, int I1>
-__device__ __forceinline__ void apply_counts(float (&v)[EPT], int lo, int hi, int tlo, const SamplingParams& p) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = I0; i < I1; ++i) {
-        const int id0 = lo + 4 * (i * WG + tid);
-        if (id0 >= hi) continue;
-        const int t = id0 - tlo;  // a multiple of 4
-        uint32_t c[4];
-        if (C16) {
-            const uint2 q = *reinterpret_cast<const uint2*>(s_cnt + (t >> 1));
-            c[0] = q.x & 0xffffu;
-            c[1] = q.x >> 16;
-            c[2] = q.y & 0xffffu;
-            c[3] = q.y >> 16;
-        } else {
-            const uint4 q = *reinterpret_cast<const uint4*>(s_cnt + t);
-            c[0] = q.x;
-            c[1] = q.y;
-            c[2] = q.z;
-            c[3] = q.w;
-        }
-#pragma unroll
-        for (int e = 1; e < 4; ++e)
-            if (id0 + e >= hi) c[e] = 0u;
-        if ((c[0] | c[1] | c[2] | c[3]) != 0u) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (c[e] != 0u) v[4 * i + e] = penalize(v[4 * i + e], c[e], p);
-        }
+// Applies the table's counts to the four logits of group i this thread holds (ids lo + 4*(i*WG + tid) + e).
+// Nearly every wave-wide group holds some history id, so the penalty is computed for all four logits and
+// selected where the count is nonzero (no divergent branches). INR: every id is below hi.
+template <int WG, int EPT, bool C16, bool INR>
+__device__ __forceinline__ void apply_group(float (&v)[EPT], int i, int lo, int hi, int tlo, const SamplingParams& p) {
+    const int id0 = lo + 4 * (i * WG + (int) threadIdx.x);
+    if (!INR && id0 >= hi) return;
+    const int t = id0 - tlo;  // a multiple of 4
+    uint32_t c[4];
+    if (C16) {
+        const uint2 q = *reinterpret_cast<const uint2*>(s_cnt + (t >> 1));
+        c[0] = q.x & 0xffffu;
+        c[1] = q.x >> 16;
+        c[2] = q.y & 0xffffu;
+        c[3] = q.y >> 16;
+    } else {
+        const uint4 q = *reinterpret_cast<const uint4*>(s_cnt + t);
+        c[0] = q.x;
+        c[1] = q.y;
+        c[2] = q.z;
+        c[3] = q.w;
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (!INR && id0 + e >= hi) c[e] = 0u;
+        const float x = v[4 * i + e];
+        const float y = penalize(x, c[e], p);
+        v[4 * i + e] = c[e] != 0u ? y : x;
+    }
+}
+
+template <int WG, int EPT, bool C16, bool INR, int I0, int I1>
+__device__ __forceinline__ void apply_counts(float (&v)[EPT], int lo, int hi, int tlo, const SamplingParams& p) {
+#pragma unroll
+    for (int i = I0; i < I1; ++i) apply_group<WG, EPT, C16, INR>(v, i, lo, hi, tlo, p);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -528,19 +537,20 @@ __device__ __forceinline__ void scan_exact(WaveTopK<NW>& w, const RowsArgs& a, c
 // Slow path of a segment (a region overflowed, e.g. many logits equal to the bound): re-read the segment and
 // keep exact per-wave lists with folding, then merge. With `wide` counts the history is staged again, half a
 // segment at a time. Returns the top-64 in wave 0.
+// The table, when present, covers the ids from lb (<= lo) on.
 template <int NW, int SEG, bool C16>
 __device__ __forceinline__ uint64_t segment_slow(const RowsArgs& a, const float* __restrict__ L, int row, int lo, int hi,
-                                                 bool pen, bool wide, const RawHistory& rh, uint64_t t_row, int lane,
-                                                 int wave) {
+                                                 int lb, bool pen, bool wide, const RawHistory& rh, uint64_t t_row,
+                                                 int lane, int wave) {
     constexpr int WG = NW * 64;
     WaveTopK<NW> w;
     if (!pen || !wide) {
-        scan_exact<NW, C16>(w, a, L, lo, hi, pen, lo, t_row, lane, wave);
+        scan_exact<NW, C16>(w, a, L, lo, hi, pen, lb, t_row, lane, wave);
     } else {
 #pragma unroll 1
         for (int h = 0; h < 2; ++h) {
-            const int wlo = lo + h * (SEG / 2), whi = min(hi, wlo + SEG / 2);
-            if (wlo >= hi) break;
+            const int wlo = max(lo, lb + h * (SEG / 2)), whi = min(hi, lb + (h + 1) * (SEG / 2));
+            if (wlo >= whi) continue;  // uniform
             __syncthreads();
             cnt_zero<WG>(whi - wlo);
             __syncthreads();
@@ -695,7 +705,39 @@ __device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok) {
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-template <bool GREEDY, bool PENALIZE, int NW, int EPT>
+// Loads this thread's logits of groups I0 <= i < I1: ids lb + 4*(i*WG + tid) + e.
+//  * FULL: every group is a whole aligned float4 inside the row, read through the buffer resource `seg` (base =
+//    logit lb) with one offset register for all groups;
+//  * otherwise each float4 is checked against hi (NaN past it) and misaligned rows load scalars.
+template <bool FULL, int WG, int EPT, int I0, int I1>
+__device__ __forceinline__ void load_groups(float (&v)[EPT], bool vec, __amdgpu_buffer_rsrc_t seg,
+                                            const float* __restrict__ L, int lb, int hi) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+        if constexpr (FULL) {
+            const u32x4 f = __builtin_amdgcn_raw_buffer_load_b128(seg, tid * 16, i * WG * 16, kNonTemporal);
+            v[4 * i + 0] = __uint_as_float(f[0]);
+            v[4 * i + 1] = __uint_as_float(f[1]);
+            v[4 * i + 2] = __uint_as_float(f[2]);
+            v[4 * i + 3] = __uint_as_float(f[3]);
+        } else {
+            const int base = lb + 4 * (i * WG + tid);
+            if (vec && base + 3 < hi) {
+                const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(L + base));
+                v[4 * i + 0] = f[0];
+                v[4 * i + 1] = f[1];
+                v[4 * i + 2] = f[2];
+                v[4 * i + 3] = f[3];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * i + e] = (base + e < hi) ? L[base + e] : __uint_as_float(0x7fc00000u);
+            }
+        }
+    }
+}
+
+template <bool GREEDY, bool PENALIZE, bool FULL, int NW, int EPT>
 __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     constexpr int WG = NW * 64;
     constexpr int SEG = WG * EPT;
@@ -714,9 +756,15 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         item = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     }
     if (item >= a.n_rows * a.segs) return;
-    const int row = item / a.segs, seg = item - row * a.segs;
+    // (uniform; readfirstlane keeps the row and the addresses derived from it in scalar registers)
+    const int row = __builtin_amdgcn_readfirstlane(item / a.segs), seg = item - row * a.segs;
     const int lo = seg * SEG;
     const int hi = min(a.V, lo + SEG);
+    // FULL (V >= SEG, aligned rows, V % 4 == 0): every workgroup reads SEG whole float4s; the row's last segment
+    // is shifted down to end at V, and its ids below lo (the previous segment's) are masked to NaN as they are
+    // first used. lb is the first id held.
+    const int lb = FULL ? min(lo, a.V - SEG) : lo;
+    const int skip = lo - lb;  // leading ids held but not owned (uniform)
     const float* __restrict__ L = a.logits + (int64_t) row * a.row_stride;
     const bool vec = ((a.row_stride & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0);
     const int k = a.p.k;
@@ -725,68 +773,66 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     const uint64_t t_row =
         a.share_bounds ? __hip_atomic_load(&a.row_thr[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
 
-    // ---- one coalesced read of the segment: thread t holds ids lo + 4*(i*WG + t) + e. The first half is
-    // issued before anything that waits on memory; the row's raw history (a prefetch into registers) goes
-    // between the halves, so its counts are staged while the second half is in flight.
+    // ---- one coalesced read of the segment: thread t holds ids lb + 4*(i*WG + t) + e, in three batches. With
+    // penalties the row's raw history is prefetched (into registers) after the first quarter and counted into
+    // the LDS table while the middle half is in flight; the last quarter is issued after the count, so the
+    // prefetched ids and the whole segment are never held at once.
+    const __amdgpu_buffer_rsrc_t seg_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(L + lb), (short) 0, SEG * 4, kRawBufferFlags);
+    constexpr int Q1 = PENALIZE ? NV / 4 : NV, Q3 = PENALIZE ? NV - NV / 4 : NV;
     float v[EPT];
-    int4 hq[HR];
-#pragma unroll
-    for (int r = 0; r < HR; ++r) hq[r] = make_int4(-1, -1, -1, -1);
     RawHistory rh;
     bool wide = false;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        if (PENALIZE && i == NVH) {
-            if (a.hist_off) {
-                rh.s0 = max(a.hist_off[row], 0);
-                rh.s1 = max(a.hist_off[row + 1], rh.s0);
-                const bool hv = (reinterpret_cast<uintptr_t>(a.hist_ids) & 15u) == 0;
-                rh.b0 = hv ? min(rh.s1, (rh.s0 + 3) & ~3) : rh.s1;
-                rh.b1 = hv ? max(rh.b0, rh.s1 & ~3) : rh.s1;
-#pragma unroll
-                for (int r = 0; r < HR; ++r) {
-                    const int j = rh.b0 + 4 * (r * WG + tid);
-                    if (j < rh.b1) hq[r] = *reinterpret_cast<const int4*>(a.hist_ids + j);
-                }
-            }
-            // counts reach 65536 only with that many history ids in the row (extras included)
-            const int extra = (a.extra_a ? PENDING_CAP : 0) + (a.extra_b ? VERIFY_MAX_ROWS : 0);
-            wide = C16 && (a.count_wide != 0 || (rh.s1 - rh.s0) + extra >= 65536);
-            if (!wide) cnt_zero<WG>(C16 ? (hi - lo + 1) / 2 : hi - lo);
-        }
-        const int base = lo + 4 * (i * WG + tid);
-        if (vec && base + 3 < hi) {
-            const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(L + base));
-            v[4 * i + 0] = f[0];
-            v[4 * i + 1] = f[1];
-            v[4 * i + 2] = f[2];
-            v[4 * i + 3] = f[3];
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * i + e] = (base + e < hi) ? L[base + e] : __uint_as_float(0x7fc00000u);
-        }
-    }
+    load_groups<FULL, WG, EPT, 0, Q1>(v, vec, seg_rsrc, L, lb, hi);
     if (PENALIZE) {
+        int4 hq[HR];
+#pragma unroll
+        for (int r = 0; r < HR; ++r) hq[r] = make_int4(-1, -1, -1, -1);
+        if (a.hist_off) {
+            rh.s0 = max(a.hist_off[row], 0);
+            rh.s1 = max(a.hist_off[row + 1], rh.s0);
+            const bool hv = (reinterpret_cast<uintptr_t>(a.hist_ids) & 15u) == 0;
+            rh.b0 = hv ? min(rh.s1, (rh.s0 + 3) & ~3) : rh.s1;
+            rh.b1 = hv ? max(rh.b0, rh.s1 & ~3) : rh.s1;
+#pragma unroll
+            for (int r = 0; r < HR; ++r) {
+                const int j = rh.b0 + 4 * (r * WG + tid);
+                if (j < rh.b1) hq[r] = *reinterpret_cast<const int4*>(a.hist_ids + j);
+            }
+        }
+        // counts reach 65536 only with that many history ids in the row (extras included)
+        const int extra = (a.extra_a ? PENDING_CAP : 0) + (a.extra_b ? VERIFY_MAX_ROWS : 0);
+        wide = C16 && (a.count_wide != 0 || (rh.s1 - rh.s0) + extra >= 65536);
+        if (!wide) cnt_zero<WG>(C16 ? (hi - lb + 1) / 2 : hi - lb);
+        load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
         if (!wide) {
             __syncthreads();  // table zeroed
-            count_history<WG, C16, true>(a, row, lo, hi, hq, rh);
-            __syncthreads();
-            apply_counts<WG, EPT, C16, 0, NV>(v, lo, hi, lo, a.p);
+            count_history<WG, C16, true>(a, row, lb, hi, hq, rh);
+        }
+    }
+    load_groups<FULL, WG, EPT, Q3, NV>(v, vec, seg_rsrc, L, lb, hi);
+    // with penalties (16-bit or narrow tables) the counts are applied group by group as the logits are first
+    // used, below; wide counts are applied here, half a segment at a time
+    const bool pen_now = PENALIZE && !wide;
+    if (PENALIZE) {
+        if (!wide) {
+            __syncthreads();  // table complete
         } else if constexpr (C16) {
-            // 32-bit counts over half a segment at a time
-            const int mid = min(hi, lo + SEG / 2);
-            cnt_zero<WG>(mid - lo);
+            // 32-bit counts over half a segment at a time, the history read again from memory
+            const int4 none[HR] = {};
+            const int mid = min(hi, lb + SEG / 2);
+            cnt_zero<WG>(mid - lb);
             __syncthreads();
-            count_history<WG, false, true>(a, row, lo, mid, hq, rh);
+            count_history<WG, false, false>(a, row, lb, mid, none, rh);
             __syncthreads();
-            apply_counts<WG, EPT, false, 0, NV / 2>(v, lo, hi, lo, a.p);
+            apply_counts<WG, EPT, false, FULL, 0, NV / 2>(v, lb, hi, lb, a.p);
             if (mid < hi) {
                 __syncthreads();
                 cnt_zero<WG>(hi - mid);
                 __syncthreads();
-                count_history<WG, false, true>(a, row, mid, hi, hq, rh);
+                count_history<WG, false, false>(a, row, mid, hi, none, rh);
                 __syncthreads();
-                apply_counts<WG, EPT, false, NV / 2, NV>(v, lo, hi, mid, a.p);
+                apply_counts<WG, EPT, false, FULL, NV / 2, NV>(v, lb, hi, mid, a.p);
             }
         }
     }
@@ -796,13 +842,17 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         float best_v = -INFINITY;
         int best_id = 0;
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
+        for (int i = 0; i < NV; ++i) {
+            if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (v[4 * i + e] > best_v) {
+            for (int e = 0; e < 4; ++e) {
+                const int off = 4 * (i * WG + tid) + e;
+                if (v[4 * i + e] > best_v && !(FULL && off < skip)) {
                     best_v = v[4 * i + e];
-                    best_id = lo + 4 * (i * WG + tid) + e;
+                    best_id = lb + off;
                 }
+            }
+        }
         uint64_t key = best_v > -INFINITY ? mk_key(best_v, best_id) : 0ull;
         key = wave_max64(key, lane);
         if (lane == 0) s_red<NW>[wave] = key;
@@ -820,10 +870,15 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // and the waves' lists are merged (in groups of four for 16 waves).
         float m1 = -INFINITY, m2 = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            const float x = v[i] == v[i] ? v[i] : -INFINITY;
-            m2 = fmaxf(m2, fminf(m1, x));
-            m1 = fmaxf(m1, x);
+        for (int i = 0; i < NV; ++i) {
+            if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (FULL && 4 * (i * WG + tid) + e < skip) v[4 * i + e] = __uint_as_float(0x7fc00000u);
+                const float x = v[4 * i + e] == v[4 * i + e] ? v[4 * i + e] : -INFINITY;
+                m2 = fmaxf(m2, fminf(m1, x));
+                m1 = fmaxf(m1, x);
+            }
         }
         const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
         const uint32_t l2 = sort32<false>(ord_f32(m2), lane);
@@ -852,19 +907,22 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // ---- filter: one compare per logit; survivors go to the wave's LDS region
         WaveCollect<NW> w;
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
+        for (int i = 0; i < NV; ++i) {
+            const bool any = (v[4 * i] >= t_f) | (v[4 * i + 1] >= t_f) | (v[4 * i + 2] >= t_f) | (v[4 * i + 3] >= t_f);
+            if (!ballot(any)) continue;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float x = v[4 * i + e];
                 const bool pass = x >= t_f;
                 if (ballot(pass)) {
-                    const uint64_t key = mk_key(x, lo + 4 * (i * WG + tid) + e);
+                    const uint64_t key = mk_key(x, lb + 4 * (i * WG + tid) + e);
                     w.offer(wave, pass && key > t_row, key);
                 }
             }
+        }
         uint64_t lst;
         if (!wg_select<NW>(w, lane, wave, &lst))
-            lst = segment_slow<NW, SEG, C16>(a, L, row, lo, hi, PENALIZE, wide, rh, t_row, lane, wave);
+            lst = segment_slow<NW, SEG, C16>(a, L, row, lo, hi, lb, PENALIZE, wide, rh, t_row, lane, wave);
         if (wave == 0) {
             if (lane < k) store_dev(&seg_out[lane], lst);
             if (a.share_bounds) {
@@ -970,32 +1028,40 @@ constexpr size_t table_bytes() {
     return P ? (size_t) NW * 64 * EPT * (NW > 4 ? 2 : 4) : 0;
 }
 
-template <bool G, bool P, int NW, int EPT>
+template <bool G, bool P, bool F, int NW, int EPT>
 hipError_t launch_cfg(const RowsArgs& a, hipStream_t s) {
     constexpr size_t lds = table_bytes<P, NW, EPT>();
-    hipLaunchKernelGGL((rows_kernel<G, P, NW, EPT>), dim3(rows_grid(a)), dim3(NW * 64), lds, s, a);
+    hipLaunchKernelGGL((rows_kernel<G, P, F, NW, EPT>), dim3(rows_grid(a)), dim3(NW * 64), lds, s, a);
     return hipGetLastError();
 }
 
-template <bool G, bool P>
-hipError_t launch_gp(const RowsArgs& a, hipStream_t s) {
+template <bool G, bool P, bool F>
+hipError_t launch_gpf(const RowsArgs& a, hipStream_t s) {
     switch (a.seg_len) {
-        case 1024: return launch_cfg<G, P, 4, 4>(a, s);
-        case 2048: return launch_cfg<G, P, 4, 8>(a, s);
-        case 4096: return launch_cfg<G, P, 4, 16>(a, s);
-        case 8192: return launch_cfg<G, P, 4, 32>(a, s);
-        case 16384: return launch_cfg<G, P, 16, 16>(a, s);
-        case 32768: return launch_cfg<G, P, 16, 32>(a, s);
-        case 65536: return launch_cfg<G, P, 16, 64>(a, s);
+        case 1024: return launch_cfg<G, P, F, 4, 4>(a, s);
+        case 2048: return launch_cfg<G, P, F, 4, 8>(a, s);
+        case 4096: return launch_cfg<G, P, F, 4, 16>(a, s);
+        case 8192: return launch_cfg<G, P, F, 4, 32>(a, s);
+        case 16384: return launch_cfg<G, P, F, 16, 16>(a, s);
+        case 32768: return launch_cfg<G, P, F, 16, 32>(a, s);
+        case 65536: return launch_cfg<G, P, F, 16, 64>(a, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-template <bool G, bool P, int NW, int EPT>
+template <bool G, bool P>
+hipError_t launch_gp(const RowsArgs& a, hipStream_t s) {
+    // whole aligned float4s everywhere: the row start and stride allow 16-byte loads and no segment is partial
+    const bool full = ((a.row_stride & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0) &&
+                      (a.V & 3) == 0 && a.V >= a.seg_len;
+    return full ? launch_gpf<G, P, true>(a, s) : launch_gpf<G, P, false>(a, s);
+}
+
+template <bool G, bool P, bool F, int NW, int EPT>
 hipError_t allow_lds() {
     constexpr size_t b = table_bytes<P, NW, EPT>();
     if (b <= 65536) return hipSuccess;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&rows_kernel<G, P, NW, EPT>),
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&rows_kernel<G, P, F, NW, EPT>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int) b);
 }
 
@@ -1007,8 +1073,10 @@ int rows_grid(const RowsArgs& a) {
 }
 
 hipError_t prepare_rows_kernels() {
-    hipError_t e = allow_lds<false, true, 16, 64>();
-    if (e == hipSuccess) e = allow_lds<true, true, 16, 64>();
+    hipError_t e = allow_lds<false, true, false, 16, 64>();
+    if (e == hipSuccess) e = allow_lds<true, true, false, 16, 64>();
+    if (e == hipSuccess) e = allow_lds<false, true, true, 16, 64>();
+    if (e == hipSuccess) e = allow_lds<true, true, true, 16, 64>();
     return e;
 }
 
