@@ -45,6 +45,9 @@ struct SamplingParams {
     float frequency;
     float repetition;
     int32_t k;  // effective top-k (1..KCAP on the fast path)
+    // 1 / repetition in double: RN_f32(l * inv_repetition) is RN_f32(l / repetition) for every float l (the
+    // product's relative error, below 2^-51.9, is smaller than any quotient's distance to a rounding midpoint)
+    double inv_repetition;
 };
 
 struct RowsArgs {

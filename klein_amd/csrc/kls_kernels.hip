@@ -263,11 +263,16 @@ __device__ __forceinline__ float expf_glibc(float x) {
     return __double2float_rn(y);
 }
 
-// Penalty of src/sampler.cpp:24-25 for an id seen `c` > 0 times: repetition first, then
-// l - (presence + frequency * (float)c), each operation rounded separately (no contraction). Branch-free: with a
-// repetition penalty of 1 both l/1 and l*1 are l, as the reference's skipped step leaves it.
+// Penalty of src/sampler.cpp:24-25 for an id seen `c` > 0 times: repetition first (l > 0 ? l / rep : l * rep),
+// then l - (presence + frequency * (float)c), each operation rounded separately (no contraction). Branch-free:
+// with a repetition penalty of 1 both forms give l, as the reference's skipped step leaves it. The quotient is
+// RN_f32(l * (1/rep in double)): exact for every float l. Why: the double product's relative error is below
+// 2^-51.9, while a quotient of two floats that is not a float lies more than 2^-49 (relative) from every midpoint
+// between floats (the midpoint m = M 2^e, M odd with 25 bits, makes l - rep*m a nonzero multiple of 2^e*ulp), so
+// rounding the product to float cannot cross one. Specials agree too (0, inf, NaN operands and rep = 0 or inf).
 __device__ __forceinline__ float penalize(float l, uint32_t c, const SamplingParams& p) {
-    const float d = __fdiv_rn(l, p.repetition), m = __fmul_rn(l, p.repetition);
+    const float d = __double2float_rn(__dmul_rn((double) l, p.inv_repetition));
+    const float m = __fmul_rn(l, p.repetition);
     l = l > 0.0f ? d : m;
     const float f = __fmul_rn(p.frequency, __uint2float_rn(c));
     const float t = __fadd_rn(p.presence, f);
@@ -489,15 +494,17 @@ __device__ __forceinline__ bool wg_select(const WaveCollect<NW>& w, int lane, in
     }
     uint64_t lst = 0ull;
     if (wave < nc) {
-        // chunk `wave` of the concatenated regions
+        // chunk `wave` of the concatenated regions: find the region of entry j, then one read
         const int j = 64 * wave + lane;
-        uint64_t key = 0ull;
-        int base = 0;
+        int r = 0, base = 0, end = cnt[0];
 #pragma unroll
-        for (int r = 0; r < NW; ++r) {
-            if (j >= base && j < base + cnt[r]) key = s_cand<NW>[r][j - base];
-            base += cnt[r];
+        for (int q = 1; q < NW; ++q) {
+            const bool past = j >= end;
+            r = past ? q : r;
+            base = past ? end : base;
+            end += cnt[q];
         }
+        const uint64_t key = j < total ? s_cand<NW>[r][j - base] : 0ull;
         lst = sort64<true>(key, lane);
     }
     if (nc <= 1) {
@@ -705,6 +712,18 @@ __device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok) {
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// FULL segments shifted down to end at V hold `skip` leading ids of the previous segment: masked to NaN (in
+// place, by selects, only in groups that reach below skip: a uniform test).
+template <int WG, int EPT>
+__device__ __forceinline__ void mask_skipped(float (&v)[EPT], int i, int skip) {
+    const int g0 = 4 * i * WG;
+    if (skip > g0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[4 * i + e] = g0 + 4 * (int) threadIdx.x + e < skip ? __uint_as_float(0x7fc00000u) : v[4 * i + e];
+    }
+}
+
 // Loads this thread's logits of groups I0 <= i < I1: ids lb + 4*(i*WG + tid) + e.
 //  * FULL: every group is a whole aligned float4 inside the row, read through the buffer resource `seg` (base =
 //    logit lb) with one offset register for all groups;
@@ -844,14 +863,13 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
+            if (FULL) mask_skipped<WG, EPT>(v, i, skip);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int off = 4 * (i * WG + tid) + e;
-                if (v[4 * i + e] > best_v && !(FULL && off < skip)) {
+            for (int e = 0; e < 4; ++e)
+                if (v[4 * i + e] > best_v) {
                     best_v = v[4 * i + e];
-                    best_id = lb + off;
+                    best_id = lb + 4 * (i * WG + tid) + e;
                 }
-            }
         }
         uint64_t key = best_v > -INFINITY ? mk_key(best_v, best_id) : 0ull;
         key = wave_max64(key, lane);
@@ -868,16 +886,19 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // logit (NaN counts as -inf and never reaches a bound); the k-th largest of these 2*WG distinct logits is
         // reached by at least k logits of the segment. Each wave sorts its lane values and keeps its top 64,
         // and the waves' lists are merged (in groups of four for 16 waves).
+        // (canonicalized values: signaling NaNs quieted, so max ignores a NaN and med3 keeps m2, and every NaN fails
+        // the filter's compares; med3(m1, m2, x) = max(m2, min(m1, x)) for m1 >= m2)
         float m1 = -INFINITY, m2 = -INFINITY;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
+            if (FULL) mask_skipped<WG, EPT>(v, i, skip);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if (FULL && 4 * (i * WG + tid) + e < skip) v[4 * i + e] = __uint_as_float(0x7fc00000u);
-                const float x = v[4 * i + e] == v[4 * i + e] ? v[4 * i + e] : -INFINITY;
-                m2 = fmaxf(m2, fminf(m1, x));
-                m1 = fmaxf(m1, x);
+                const float x = __builtin_canonicalizef(v[4 * i + e]);
+                v[4 * i + e] = x;
+                m2 = __builtin_amdgcn_fmed3f(m1, m2, x);
+                m1 = __builtin_fmaxf(m1, x);
             }
         }
         const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
@@ -908,8 +929,8 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         WaveCollect<NW> w;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const bool any = (v[4 * i] >= t_f) | (v[4 * i + 1] >= t_f) | (v[4 * i + 2] >= t_f) | (v[4 * i + 3] >= t_f);
-            if (!ballot(any)) continue;
+            const float gmax = __builtin_fmaxf(__builtin_fmaxf(v[4 * i], v[4 * i + 1]), __builtin_fmaxf(v[4 * i + 2], v[4 * i + 3]));
+            if (!ballot(gmax >= t_f)) continue;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float x = v[4 * i + e];
@@ -960,6 +981,27 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             a.dbg_meta[row * 2 + 1] = 0;
         }
         publish(a, row, m ? key_id(m) : 0);  // all -inf / NaN: the reference returns id 0
+        return;
+    }
+
+    // Few segments: wave 0 merges the lists one after another (each is sorted, the first k entries valid).
+    if (a.segs <= 8) {
+        if (wave != 0) return;
+        uint64_t lk[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int l = s == 0 ? lane : 63 - lane;  // lists after the first are read reversed (ascending)
+            lk[s] = (s < a.segs && l < k) ? load_dev(&cand[(int64_t) s * KCAP + l]) : 0ull;
+        }
+        uint64_t lst = lk[0];
+#pragma unroll
+        for (int s = 1; s < 8; ++s)
+            if (s < a.segs) lst = merge64(lst, lk[s], lane);
+        const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
+        if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
+        const int tok = sample_tail(lst, kk, a.p, a.u[row], lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
+                                    a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
+        if (lane == 0) publish(a, row, tok);
         return;
     }
 
