@@ -352,7 +352,9 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
                   params->repetition_penalty != 1.0f;
     h->sp = SamplingParams{params->temperature, params->top_p, params->min_p, params->presence_penalty,
                            params->frequency_penalty, params->repetition_penalty, std::min(k, KCAP),
-                           1.0 / (double) params->repetition_penalty};
+                           1.0 / (double) params->repetition_penalty,
+                           (params->repetition_penalty >= 1.0f && params->presence_penalty >= 0.0f &&
+                            params->frequency_penalty >= 0.0f) ? 1 : 0};
     while (((n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift) > MAX_BUCKETS) h->bucket_shift++;
     h->n_buckets = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;
     if (const char* e = getenv("KLS_SEG_LEN")) h->seg_len_override = atoi(e);

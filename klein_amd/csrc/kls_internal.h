@@ -48,6 +48,7 @@ struct SamplingParams {
     // 1 / repetition in double: RN_f32(l * inv_repetition) is RN_f32(l / repetition) for every float l (the
     // product's relative error, below 2^-51.9, is smaller than any quotient's distance to a rounding midpoint)
     double inv_repetition;
+    int32_t lazy;  // penalties never raise a logit (repetition >= 1, presence >= 0, frequency >= 0)
 };
 
 struct RowsArgs {

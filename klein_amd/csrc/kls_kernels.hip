@@ -357,12 +357,16 @@ __device__ __forceinline__ void count_history(const RowsArgs& a, int row, int tl
 // Applies the table's counts to the four logits of group i this thread holds (ids lo + 4*(i*WG + tid) + e).
 // Nearly every wave-wide group holds some history id, so the penalty is computed for all four logits and
 // selected where the count is nonzero (no divergent branches). INR: every id is below hi.
-template <int WG, int EPT, bool C16, bool INR>
-__device__ __forceinline__ void apply_group(float (&v)[EPT], int i, int lo, int hi, int tlo, const SamplingParams& p) {
+// The history counts of the four ids lo + 4*(i*WG + tid) + e from the table over [tlo, ...); 0 past hi (unless
+// INR: every id is below hi).
+template <int WG, bool C16, bool INR>
+__device__ __forceinline__ void group_counts(uint32_t (&c)[4], int i, int lo, int hi, int tlo) {
     const int id0 = lo + 4 * (i * WG + (int) threadIdx.x);
-    if (!INR && id0 >= hi) return;
+    if (!INR && id0 >= hi) {
+        c[0] = c[1] = c[2] = c[3] = 0u;
+        return;
+    }
     const int t = id0 - tlo;  // a multiple of 4
-    uint32_t c[4];
     if (C16) {
         const uint2 q = *reinterpret_cast<const uint2*>(s_cnt + (t >> 1));
         c[0] = q.x & 0xffffu;
@@ -377,8 +381,16 @@ __device__ __forceinline__ void apply_group(float (&v)[EPT], int i, int lo, int 
         c[3] = q.w;
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 1; e < 4; ++e)
         if (!INR && id0 + e >= hi) c[e] = 0u;
+}
+
+template <int WG, int EPT, bool C16, bool INR>
+__device__ __forceinline__ void apply_group(float (&v)[EPT], int i, int lo, int hi, int tlo, const SamplingParams& p) {
+    uint32_t c[4];
+    group_counts<WG, C16, INR>(c, i, lo, hi, tlo);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
         const float x = v[4 * i + e];
         const float y = penalize(x, c[e], p);
         v[4 * i + e] = c[e] != 0u ? y : x;
@@ -832,7 +844,11 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     load_groups<FULL, WG, EPT, Q3, NV>(v, vec, seg_rsrc, L, lb, hi);
     // with penalties (16-bit or narrow tables) the counts are applied group by group as the logits are first
     // used, below; wide counts are applied here, half a segment at a time
-    const bool pen_now = PENALIZE && !wide;
+    // Penalties that never raise a logit (rep >= 1, presence >= 0, frequency >= 0: penalized <= raw for every
+    // id) are applied lazily: history ids are left out of the bounds, and only a history logit whose raw value
+    // passes a bound is penalized and tested again. Otherwise every count is applied as the logits arrive.
+    const bool pen_now = PENALIZE && !wide && !a.p.lazy;
+    const bool pen_lazy = PENALIZE && !wide && a.p.lazy;
     if (PENALIZE) {
         if (!wide) {
             __syncthreads();  // table complete
@@ -864,12 +880,17 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         for (int i = 0; i < NV; ++i) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
             if (FULL) mask_skipped<WG, EPT>(v, i, skip);
+            uint32_t c[4] = {0u, 0u, 0u, 0u};
+            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (v[4 * i + e] > best_v) {
-                    best_v = v[4 * i + e];
+            for (int e = 0; e < 4; ++e) {
+                float x = v[4 * i + e];
+                if (x > best_v && c[e] != 0u) x = penalize(x, c[e], a.p);  // lazy: penalized <= raw
+                if (x > best_v) {
+                    best_v = x;
                     best_id = lb + 4 * (i * WG + tid) + e;
                 }
+            }
         }
         uint64_t key = best_v > -INFINITY ? mk_key(best_v, best_id) : 0ull;
         key = wave_max64(key, lane);
@@ -893,12 +914,15 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         for (int i = 0; i < NV; ++i) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
             if (FULL) mask_skipped<WG, EPT>(v, i, skip);
+            uint32_t c[4] = {0u, 0u, 0u, 0u};
+            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float x = __builtin_canonicalizef(v[4 * i + e]);
                 v[4 * i + e] = x;
-                m2 = __builtin_amdgcn_fmed3f(m1, m2, x);
-                m1 = __builtin_fmaxf(m1, x);
+                const float xb = c[e] != 0u ? -INFINITY : x;  // lazy: history ids stay out of the bound
+                m2 = __builtin_amdgcn_fmed3f(m1, m2, xb);
+                m1 = __builtin_fmaxf(m1, xb);
             }
         }
         const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
@@ -931,9 +955,12 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         for (int i = 0; i < NV; ++i) {
             const float gmax = __builtin_fmaxf(__builtin_fmaxf(v[4 * i], v[4 * i + 1]), __builtin_fmaxf(v[4 * i + 2], v[4 * i + 3]));
             if (!ballot(gmax >= t_f)) continue;
+            uint32_t c[4] = {0u, 0u, 0u, 0u};
+            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float x = v[4 * i + e];
+                float x = v[4 * i + e];
+                if (x >= t_f && c[e] != 0u) x = penalize(x, c[e], a.p);  // lazy: test the penalized value
                 const bool pass = x >= t_f;
                 if (ballot(pass)) {
                     const uint64_t key = mk_key(x, lb + 4 * (i * WG + tid) + e);
