@@ -360,13 +360,16 @@ __device__ __forceinline__ void count_history(const RowsArgs& a, int row, int tl
 // The history counts of the four ids lo + 4*(i*WG + tid) + e from the table over [tlo, ...); 0 past hi (unless
 // INR: every id is below hi).
 template <int WG, bool C16, bool INR>
-__device__ __forceinline__ void group_counts(uint32_t (&c)[4], int i, int lo, int hi, int tlo) {
+__device__ __forceinline__ void group_counts(uint32_t (&c)[4], int i, int lo, int hi, int tlo, float dep = 0.0f) {
     const int id0 = lo + 4 * (i * WG + (int) threadIdx.x);
     if (!INR && id0 >= hi) {
         c[0] = c[1] = c[2] = c[3] = 0u;
         return;
     }
-    const int t = id0 - tlo;  // a multiple of 4
+    int t = id0 - tlo;  // a multiple of 4
+    // The read waits for `dep` (the caller's running result over the previous groups): the scheduler would
+    // otherwise hoist every group's read ahead of the data and hold all their flags at once.
+    asm volatile("" : "+v"(t) : "v"(dep));
     if (C16) {
         const uint2 q = *reinterpret_cast<const uint2*>(s_cnt + (t >> 1));
         c[0] = q.x & 0xffffu;
@@ -881,7 +884,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
             if (FULL) mask_skipped<WG, EPT>(v, i, skip);
             uint32_t c[4] = {0u, 0u, 0u, 0u};
-            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb);
+            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb, best_v);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float x = v[4 * i + e];
@@ -915,7 +918,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
             if (FULL) mask_skipped<WG, EPT>(v, i, skip);
             uint32_t c[4] = {0u, 0u, 0u, 0u};
-            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb);
+            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb, m2);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float x = __builtin_canonicalizef(v[4 * i + e]);
