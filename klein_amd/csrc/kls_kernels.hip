@@ -808,12 +808,13 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         a.share_bounds ? __hip_atomic_load(&a.row_thr[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
 
     // ---- one coalesced read of the segment: thread t holds ids lb + 4*(i*WG + t) + e, in three batches. With
-    // penalties the row's raw history is prefetched (into registers) after the first quarter and counted into
-    // the LDS table while the middle half is in flight; the last quarter is issued after the count, so the
-    // prefetched ids and the whole segment are never held at once.
+    // penalties the row's raw history is prefetched (into registers) after the first groups of logits (its wait
+    // covers those only: loads complete in order) and counted into the LDS table while the middle of the segment
+    // is in flight; the last quarter is issued after the count, so the prefetched ids and the whole segment are
+    // never held at once.
     const __amdgpu_buffer_rsrc_t seg_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(L + lb), (short) 0, SEG * 4, kRawBufferFlags);
-    constexpr int Q1 = PENALIZE ? NV / 4 : NV, Q3 = PENALIZE ? NV - NV / 4 : NV;
+    constexpr int Q1 = PENALIZE ? (NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : NV, Q3 = PENALIZE ? NV - NV / 4 : NV;
     float v[EPT];
     RawHistory rh;
     bool wide = false;
@@ -838,10 +839,13 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         const int extra = (a.extra_a ? PENDING_CAP : 0) + (a.extra_b ? VERIFY_MAX_ROWS : 0);
         wide = C16 && (a.count_wide != 0 || (rh.s1 - rh.s0) + extra >= 65536);
         if (!wide) cnt_zero<WG>(C16 ? (hi - lb + 1) / 2 : hi - lb);
+        // (the barrier comes before the middle batch: every wave reaches it having issued few loads; a wave
+        // whose loads wait for issue slots would hold the others here)
+        __syncthreads();  // table zeroed
         load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
         if (!wide) {
-            __syncthreads();  // table zeroed
             count_history<WG, C16, true>(a, row, lb, hi, hq, rh);
+            __syncthreads();  // table complete (before the last batch, for the same reason)
         }
     }
     load_groups<FULL, WG, EPT, Q3, NV>(v, vec, seg_rsrc, L, lb, hi);
@@ -852,10 +856,8 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // passes a bound is penalized and tested again. Otherwise every count is applied as the logits arrive.
     const bool pen_now = PENALIZE && !wide && !a.p.lazy;
     const bool pen_lazy = PENALIZE && !wide && a.p.lazy;
-    if (PENALIZE) {
-        if (!wide) {
-            __syncthreads();  // table complete
-        } else if constexpr (C16) {
+    if (PENALIZE && wide) {
+        if constexpr (C16) {
             // 32-bit counts over half a segment at a time, the history read again from memory
             const int4 none[HR] = {};
             const int mid = min(hi, lb + SEG / 2);
