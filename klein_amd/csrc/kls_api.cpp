@@ -230,8 +230,9 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
     const RowsArgs a = step_args(h, dl, rows, verify);
     if (verify) {
         if (!h->g_valid || h->g_logits != dl || h->g_rows != rows) {
-            if (h->gexec) hipGraphExecDestroy(h->gexec);
-            if (h->graph) hipGraphDestroy(h->graph);
+            // (a stale graph is replaced whether or not its teardown reports an error)
+            if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
+            if (h->graph) (void) hipGraphDestroy(h->graph);
             h->gexec = nullptr;
             h->graph = nullptr;
             h->g_valid = false;

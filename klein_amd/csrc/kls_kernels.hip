@@ -41,7 +41,10 @@ template <int NW> __shared__ uint32_t s_q[NW];
 template <int NW> __shared__ int s_n[NW];
 template <int NW> __shared__ uint32_t s_mx[NW][64];    // per-wave sorted lane maxima
 template <int NW> __shared__ uint32_t s_mx4[4][64];    // their merges in groups of four waves
+template <int NW> __shared__ uint32_t s_mx2[NW][64];   // per-wave sorted second maxima (deferred penalties)
+template <int NW> __shared__ uint32_t s_mx4b[4][64];
 __shared__ int s_last;
+__shared__ int s_kept;  // deferred penalties: survivors still at or above the bound
 
 
 // ---------------------------------------------------------------------------------------------------------
@@ -65,6 +68,13 @@ __device__ __forceinline__ uint64_t mk_key(float v, int id) {
 }
 
 __device__ __forceinline__ int key_id(uint64_t k) { return (int) ~(uint32_t) k; }
+
+// mk_key for a value known not to be NaN (-0 + 0 = +0 folds the zeros)
+__device__ __forceinline__ uint64_t mk_key_num(float v, int id) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    const uint32_t o = u ^ ((uint32_t) ((int32_t) u >> 31) | 0x80000000u);
+    return ((uint64_t) o << 32) | (uint64_t) (~(uint32_t) id);
+}
 
 // Largest float f such that every value image >= o has value >= f.
 __device__ __forceinline__ float floor32(uint32_t o) { return o == 0u ? -INFINITY : unord_f32(o); }
@@ -94,7 +104,7 @@ __device__ __forceinline__ uint64_t min64(uint64_t a, uint64_t b) { return a > b
 // compute the inputs for the active lanes only.
 template <int CTRL>
 __device__ __forceinline__ int dpp(int x) {
-    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+    return __builtin_amdgcn_mov_dpp(x, CTRL, 0xf, 0xf, false);
 }
 
 template <int M>
@@ -140,13 +150,64 @@ __device__ __forceinline__ float rdlanef(float x, int l) {
 }
 __device__ __forceinline__ int rdlanei(int x, int l) { return __builtin_amdgcn_readlane(x, l); }
 
-// One compare-exchange step of a bitonic network over one 64-bit key per lane.
+// Lanes that keep the larger key in a compare-exchange step of a bitonic network (block size SIZE, partner
+// lane ^ STRIDE; DESC: blocks sorted descending at the end), as a wave-uniform 64-bit mask. Wave lanes are
+// numbered 0..63, so the mask is a constant and each step's direction logic is one scalar XOR.
+template <int SIZE, int STRIDE, bool DESC>
+constexpr uint64_t keep_max_lanes() {
+    uint64_t m = 0;
+    for (int l = 0; l < 64; ++l) {
+        const bool up = ((l & SIZE) == 0) == DESC;
+        const bool lower = (l & STRIDE) == 0;
+        if (lower == up) m |= 1ull << l;
+    }
+    return m;
+}
+
+// Both lanes of every pair (lane, lane ^ M), M = 16 or 32, get {lower lane's x, upper lane's x}.
+template <int M>
+__device__ __forceinline__ auto swap_rows(uint32_t x) {
+    if constexpr (M == 16) {
+        return __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    } else {
+        static_assert(M == 32, "row distance");
+        return __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    }
+}
+
+// One compare-exchange step. With DPP partners (STRIDE < 16) a lane takes its partner's key y when
+// (y > x) == keep-max; permlane swaps (STRIDE 16, 32) give both lanes of a pair the pair's lower-lane key a and
+// upper-lane key b, and a lane takes a when (a > b) == keep-max. (Equal keys: either choice is the same key.)
+template <int SIZE, int STRIDE, bool DESC, typename T>
+__device__ __forceinline__ T bitonic_step_t(T x, int lane) {
+    const bool km = __builtin_amdgcn_inverse_ballot_w64(keep_max_lanes<SIZE, STRIDE, DESC>());
+    if constexpr (STRIDE < 16) {
+        T y;
+        if constexpr (sizeof(T) == 8) {
+            y = xor_lane64<STRIDE>(x, lane);
+        } else {
+            y = (T) xor_lane<STRIDE>((int) x, lane);
+        }
+        return ((y > x) == km) ? y : x;
+    } else {
+        T a, b;
+        if constexpr (sizeof(T) == 8) {
+            const auto pl = swap_rows<STRIDE>((uint32_t) x);
+            const auto ph = swap_rows<STRIDE>((uint32_t) (x >> 32));
+            a = ((uint64_t) ph[0] << 32) | pl[0];
+            b = ((uint64_t) ph[1] << 32) | pl[1];
+        } else {
+            const auto p = swap_rows<STRIDE>(x);
+            a = p[0];
+            b = p[1];
+        }
+        return ((a > b) == km) ? a : b;
+    }
+}
+
 template <int SIZE, int STRIDE, bool DESC>
 __device__ __forceinline__ uint64_t bitonic_step(uint64_t x, int lane) {
-    const uint64_t y = xor_lane64<STRIDE>(x, lane);
-    const bool up = (((lane & SIZE) == 0) == DESC);
-    const bool lower = (lane & STRIDE) == 0;
-    return (lower == up) ? max64(x, y) : min64(x, y);
+    return bitonic_step_t<SIZE, STRIDE, DESC, uint64_t>(x, lane);
 }
 
 template <int SIZE, bool DESC>
@@ -177,10 +238,7 @@ __device__ __forceinline__ uint64_t merge64(uint64_t a, uint64_t b, int lane) {
 
 template <int SIZE, int STRIDE, bool DESC>
 __device__ __forceinline__ uint32_t bitonic_step32(uint32_t x, int lane) {
-    const uint32_t y = (uint32_t) xor_lane<STRIDE>((int) x, lane);
-    const bool up = (((lane & SIZE) == 0) == DESC);
-    const bool lower = (lane & STRIDE) == 0;
-    return (lower == up) ? max(x, y) : min(x, y);
+    return bitonic_step_t<SIZE, STRIDE, DESC, uint32_t>(x, lane);
 }
 
 template <int SIZE, bool DESC>
@@ -357,6 +415,38 @@ __device__ __forceinline__ void count_history(const RowsArgs& a, int row, int tl
 // Applies the table's counts to the four logits of group i this thread holds (ids lo + 4*(i*WG + tid) + e).
 // Nearly every wave-wide group holds some history id, so the penalty is computed for all four logits and
 // selected where the count is nonzero (no divergent branches). INR: every id is below hi.
+// Deferred penalties: a hash of the segment's filter survivors (open addressing, id -> count) in the top of the
+// count-table region, words [HB, HB + 2^HL) ids (empty: all ones; history ids are non-negative) and
+// [HB + 2^HL, HB + 2^(HL+1)) counts.
+template <int HB, int HL>
+__device__ __forceinline__ void hash_insert(int id) {
+    uint32_t sl = ((uint32_t) id * 2654435761u) >> (32 - HL);
+    for (;;) {
+        const uint32_t prev = atomicCAS(&s_cnt[HB + sl], 0xffffffffu, (uint32_t) id);
+        if (prev == 0xffffffffu || prev == (uint32_t) id) return;
+        sl = (sl + 1u) & ((1u << HL) - 1u);
+    }
+}
+
+template <int HB, int HL>
+__device__ __forceinline__ int hash_find(int id) {
+    uint32_t sl = ((uint32_t) id * 2654435761u) >> (32 - HL);
+    for (;;) {
+        const uint32_t h = s_cnt[HB + sl];
+        if (h == (uint32_t) id) return (int) sl;
+        if (h == 0xffffffffu) return -1;
+        sl = (sl + 1u) & ((1u << HL) - 1u);
+    }
+}
+
+// Counts one history id into its survivor's slot (ids outside [lo, hi) and ids that did not survive are skipped).
+template <int HB, int HL>
+__device__ __forceinline__ void hash_count(int id, int lo, int hi) {
+    if ((uint32_t) id - (uint32_t) lo >= (uint32_t) (hi - lo)) return;
+    const int sl = hash_find<HB, HL>(id);
+    if (sl >= 0) atomicAdd(&s_cnt[HB + (1 << HL) + sl], 1u);
+}
+
 // The history counts of the four ids lo + 4*(i*WG + tid) + e from the table over [tlo, ...); 0 past hi (unless
 // INR: every id is below hi).
 template <int WG, bool C16, bool INR>
@@ -483,29 +573,32 @@ __device__ __forceinline__ uint64_t merge_lists(int n, int lane, int wave) {
 
 // The workgroup's descending top-64 of what its waves collected, in wave 0 (other waves get 0). Returns false
 // (in every thread) if a region overflowed.
+// Publishes the waves' region counts (-1: overflow) and reads them all back; returns false if any overflowed.
 template <int NW>
-__device__ __forceinline__ bool wg_select(const WaveCollect<NW>& w, int lane, int wave, uint64_t* out) {
+__device__ __forceinline__ bool region_counts(const WaveCollect<NW>& w, int lane, int wave, int (&cnt)[NW], int* total) {
     if (lane == 0) s_n<NW>[wave] = w.overflow ? -1 : w.n;
     __syncthreads();
-    int cnt[NW];
-    int total = 0;
     bool bad = false;
+    *total = 0;
 #pragma unroll
     for (int r = 0; r < NW; ++r) {
         cnt[r] = s_n<NW>[r];
         bad |= cnt[r] < 0;
-        total += cnt[r];
+        *total += cnt[r];
     }
-    *out = 0ull;
-    if (bad) return false;
+    return !bad;
+}
+
+// The workgroup's descending top-64 of the regions (cnt[r] keys in region r), in wave 0 (others get 0).
+template <int NW>
+__device__ __forceinline__ uint64_t select_regions(const int (&cnt)[NW], int total, int lane, int wave) {
     const int nc = (total + 63) >> 6;
     if (nc > NW) {
         // more chunks than waves: every wave folds its own region, wave 0 merges the lists
         const uint64_t lst = fold_region<NW>(wave, s_n<NW>[wave], 0ull, false, lane);
         s_list<NW>[wave][lane] = lst;
         __syncthreads();
-        *out = merge_lists<NW>(NW, lane, wave);
-        return true;
+        return merge_lists<NW>(NW, lane, wave);
     }
     uint64_t lst = 0ull;
     if (wave < nc) {
@@ -522,13 +615,20 @@ __device__ __forceinline__ bool wg_select(const WaveCollect<NW>& w, int lane, in
         const uint64_t key = j < total ? s_cand<NW>[r][j - base] : 0ull;
         lst = sort64<true>(key, lane);
     }
-    if (nc <= 1) {
-        *out = wave == 0 ? lst : 0ull;
-        return true;
-    }
+    if (nc <= 1) return wave == 0 ? lst : 0ull;
     if (wave < nc) s_list<NW>[wave][lane] = lst;
     __syncthreads();
-    *out = merge_lists<NW>(nc, lane, wave);
+    return merge_lists<NW>(nc, lane, wave);
+}
+
+// The workgroup's descending top-64 of what its waves collected, in wave 0 (other waves get 0). Returns false
+// (in every thread) if a region overflowed.
+template <int NW>
+__device__ __forceinline__ bool wg_select(const WaveCollect<NW>& w, int lane, int wave, uint64_t* out) {
+    int cnt[NW], total;
+    *out = 0ull;
+    if (!region_counts<NW>(w, lane, wave, cnt, &total)) return false;
+    *out = select_regions<NW>(cnt, total, lane, wave);
     return true;
 }
 
@@ -727,18 +827,6 @@ __device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok) {
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// FULL segments shifted down to end at V hold `skip` leading ids of the previous segment: masked to NaN (in
-// place, by selects, only in groups that reach below skip: a uniform test).
-template <int WG, int EPT>
-__device__ __forceinline__ void mask_skipped(float (&v)[EPT], int i, int skip) {
-    const int g0 = 4 * i * WG;
-    if (skip > g0) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            v[4 * i + e] = g0 + 4 * (int) threadIdx.x + e < skip ? __uint_as_float(0x7fc00000u) : v[4 * i + e];
-    }
-}
-
 // Loads this thread's logits of groups I0 <= i < I1: ids lb + 4*(i*WG + tid) + e.
 //  * FULL: every group is a whole aligned float4 inside the row, read through the buffer resource `seg` (base =
 //    logit lb) with one offset register for all groups;
@@ -795,8 +883,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     const int lo = seg * SEG;
     const int hi = min(a.V, lo + SEG);
     // FULL (V >= SEG, aligned rows, V % 4 == 0): every workgroup reads SEG whole float4s; the row's last segment
-    // is shifted down to end at V, and its ids below lo (the previous segment's) are masked to NaN as they are
-    // first used. lb is the first id held.
+    // is shifted down to end at V, so it also holds `skip` ids below lo (the previous segment's). Those take part
+    // in the maximum and the bound (real logits of the row: a bound that k held logits reach is one that k logits
+    // of the row reach, and a repeated maximum is harmless) but are never offered as candidates, so each id is
+    // listed by one segment only. lb is the first id held.
     const int lb = FULL ? min(lo, a.V - SEG) : lo;
     const int skip = lo - lb;  // leading ids held but not owned (uniform)
     const float* __restrict__ L = a.logits + (int64_t) row * a.row_stride;
@@ -881,12 +971,13 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // src/sampler.cpp:31-39: a thread's ids ascend with (i, e), so strict '>' keeps the lowest id.
         float best_v = -INFINITY;
         int best_id = 0;
+        uint32_t cn[4] = {0u, 0u, 0u, 0u};  // lazy: group i+1's counts, read while group i is worked on
+        if (pen_lazy) group_counts<WG, C16, FULL>(cn, 0, lb, hi, lb, best_v);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
-            if (FULL) mask_skipped<WG, EPT>(v, i, skip);
-            uint32_t c[4] = {0u, 0u, 0u, 0u};
-            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb, best_v);
+            const uint32_t c[4] = {cn[0], cn[1], cn[2], cn[3]};
+            if (pen_lazy && i + 1 < NV) group_counts<WG, C16, FULL>(cn, i + 1, lb, hi, lb, best_v);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float x = v[4 * i + e];
@@ -915,31 +1006,42 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // (canonicalized values: signaling NaNs quieted, so max ignores a NaN and med3 keeps m2, and every NaN fails
         // the filter's compares; med3(m1, m2, x) = max(m2, min(m1, x)) for m1 >= m2)
         float m1 = -INFINITY, m2 = -INFINITY;
+        float hm = -INFINITY;  // lazy: largest raw logit of a history id
+        int s1 = 0;            // slot 4*i+e of m1 (its first occurrence)
+        // lazy: the counts of group i+1 are read while group i is worked on
+        uint32_t cn[4] = {0u, 0u, 0u, 0u};
+        if (pen_lazy) group_counts<WG, C16, FULL>(cn, 0, lb, hi, lb, m2);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
-            if (FULL) mask_skipped<WG, EPT>(v, i, skip);
-            uint32_t c[4] = {0u, 0u, 0u, 0u};
-            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb, m2);
+            const uint32_t c[4] = {cn[0], cn[1], cn[2], cn[3]};
+            if (pen_lazy && i + 1 < NV) group_counts<WG, C16, FULL>(cn, i + 1, lb, hi, lb, m2);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float x = __builtin_canonicalizef(v[4 * i + e]);
                 v[4 * i + e] = x;
                 const float xb = c[e] != 0u ? -INFINITY : x;  // lazy: history ids stay out of the bound
+                if (pen_lazy) hm = __builtin_fmaxf(hm, c[e] != 0u ? x : -INFINITY);
+                s1 = xb > m1 ? 4 * i + e : s1;
+                asm volatile("" : "+v"(s1));  // kept as a register update (not deferred per-slot compares)
                 m2 = __builtin_amdgcn_fmed3f(m1, m2, xb);
                 m1 = __builtin_fmaxf(m1, xb);
             }
         }
-        const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
-        const uint32_t l2 = sort32<false>(ord_f32(m2), lane);
-        s_mx<NW>[wave][lane] = bitonic_stage32<64, true>(max(l1, l2), lane);
-        __syncthreads();
         uint32_t gl;
         if constexpr (NW == 4) {
+            const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
+            const uint32_t l2 = sort32<false>(ord_f32(m2), lane);
+            s_mx<NW>[wave][lane] = bitonic_stage32<64, true>(max(l1, l2), lane);
+            __syncthreads();
             gl = s_mx<NW>[0][lane];
 #pragma unroll
             for (int o = 1; o < NW; ++o) gl = merge32(gl, s_mx<NW>[o][63 - lane], lane);
         } else {
+            // 16 waves: the lane maxima only (one sort per wave); groups of four lists are merged by waves 0..3,
+            // their four results by wave 0
+            s_mx<NW>[wave][lane] = sort32<true>(ord_f32(m1), lane);
+            __syncthreads();
             if (wave < 4) {
                 gl = s_mx<NW>[4 * wave][lane];
 #pragma unroll
@@ -947,31 +1049,54 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                 s_mx4<NW>[wave][lane] = gl;
             }
             __syncthreads();
-            gl = s_mx4<NW>[0][lane];
+            if (wave == 0) {
+                gl = s_mx4<NW>[0][lane];
 #pragma unroll
-            for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx4<NW>[o][63 - lane], lane);
+                for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx4<NW>[o][63 - lane], lane);
+                const uint32_t qw = (uint32_t) rdlanei((int) gl, k - 1);  // all lanes active
+                if (lane == 0) s_q<NW>[0] = qw;
+            }
+            __syncthreads();
+            gl = s_q<NW>[0];
         }
-        const uint32_t q = (uint32_t) rdlanei((int) gl, k - 1);  // all lanes active
+        const uint32_t q = NW == 4 ? (uint32_t) rdlanei((int) gl, k - 1) : gl;  // all lanes active
         const float t_f = fmaxf(floor32(q), floor64(t_row));
 
-        // ---- filter: one compare per logit; survivors go to the wave's LDS region
+        // ---- filter: survivors go to the wave's LDS region. A lane whose second largest logit (and, lazily, every
+        // history logit) is below the bound holds at most one survivor, its maximum at slot s1, offered directly;
+        // the other lanes compare every logit.
         WaveCollect<NW> w;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const float gmax = __builtin_fmaxf(__builtin_fmaxf(v[4 * i], v[4 * i + 1]), __builtin_fmaxf(v[4 * i + 2], v[4 * i + 3]));
-            if (!ballot(gmax >= t_f)) continue;
-            uint32_t c[4] = {0u, 0u, 0u, 0u};
-            if (pen_lazy) group_counts<WG, C16, FULL>(c, i, lb, hi, lb);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float x = v[4 * i + e];
-                if (x >= t_f && c[e] != 0u) x = penalize(x, c[e], a.p);  // lazy: test the penalized value
-                const bool pass = x >= t_f;
-                if (ballot(pass)) {
-                    const uint64_t key = mk_key(x, lb + 4 * (i * WG + tid) + e);
-                    w.offer(wave, pass && key > t_row, key);
-                }
+        const bool multi = (pen_lazy ? __builtin_fmaxf(m2, hm) : m2) >= t_f;
+        {
+            const int slot = 4 * ((s1 >> 2) * WG + tid) + (s1 & 3);
+            const bool pass = !multi && m1 >= t_f && slot >= skip;
+            if (ballot(pass)) {
+                const uint64_t key = mk_key_num(m1, lb + slot);
+                w.offer(wave, pass && key > t_row, key);
             }
+        }
+        // Lanes with more: one at a time, the lane's EPT logits pass through the wave's (idle) list row in LDS,
+        // so that every lane of the wave tests one of them.
+        float* const buf = reinterpret_cast<float*>(&s_list<NW>[wave][0]);
+        static_assert(EPT * sizeof(float) <= sizeof(s_list<NW>[0]), "transpose row");
+        for (uint64_t mm = ballot(multi); mm != 0ull; mm &= mm - 1) {
+            const int l = (int) __builtin_ctzll(mm);  // uniform
+            if (lane == l) {
+#pragma unroll
+                for (int i = 0; i < NV; ++i)
+                    *reinterpret_cast<float4*>(buf + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            }
+            __builtin_amdgcn_wave_barrier();
+            const int sl = min(lane, EPT - 1);  // slot of the source lane
+            float x = buf[sl];
+            const int off = 4 * ((sl >> 2) * WG + wave * 64 + l) + (sl & 3);  // its id - lb
+            if (pen_lazy && x >= t_f) {
+                const uint32_t c = C16 ? (s_cnt[off >> 1] >> ((off & 1) << 4)) & 0xffffu : s_cnt[off];
+                if (c != 0u) x = penalize(x, c, a.p);  // lazy: test the penalized value
+            }
+            const uint64_t key = mk_key_num(x, lb + off);  // (used only where x passes: not NaN)
+            w.offer(wave, lane < EPT && x >= t_f && off >= skip && key > t_row, key);
+            __builtin_amdgcn_wave_barrier();
         }
         uint64_t lst;
         if (!wg_select<NW>(w, lane, wave, &lst))
