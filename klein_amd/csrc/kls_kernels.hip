@@ -41,10 +41,7 @@ template <int NW> __shared__ uint32_t s_q[NW];
 template <int NW> __shared__ int s_n[NW];
 template <int NW> __shared__ uint32_t s_mx[NW][64];    // per-wave sorted lane maxima
 template <int NW> __shared__ uint32_t s_mx4[4][64];    // their merges in groups of four waves
-template <int NW> __shared__ uint32_t s_mx2[NW][64];   // per-wave sorted second maxima (deferred penalties)
-template <int NW> __shared__ uint32_t s_mx4b[4][64];
 __shared__ int s_last;
-__shared__ int s_kept;  // deferred penalties: survivors still at or above the bound
 
 
 // ---------------------------------------------------------------------------------------------------------
@@ -412,41 +409,6 @@ __device__ __forceinline__ void count_history(const RowsArgs& a, int row, int tl
     }
 }
 
-// Applies the table's counts to the four logits of group i this thread holds (ids lo + 4*(i*WG + tid) + e).
-// Nearly every wave-wide group holds some history id, so the penalty is computed for all four logits and
-// selected where the count is nonzero (no divergent branches). INR: every id is below hi.
-// Deferred penalties: a hash of the segment's filter survivors (open addressing, id -> count) in the top of the
-// count-table region, words [HB, HB + 2^HL) ids (empty: all ones; history ids are non-negative) and
-// [HB + 2^HL, HB + 2^(HL+1)) counts.
-template <int HB, int HL>
-__device__ __forceinline__ void hash_insert(int id) {
-    uint32_t sl = ((uint32_t) id * 2654435761u) >> (32 - HL);
-    for (;;) {
-        const uint32_t prev = atomicCAS(&s_cnt[HB + sl], 0xffffffffu, (uint32_t) id);
-        if (prev == 0xffffffffu || prev == (uint32_t) id) return;
-        sl = (sl + 1u) & ((1u << HL) - 1u);
-    }
-}
-
-template <int HB, int HL>
-__device__ __forceinline__ int hash_find(int id) {
-    uint32_t sl = ((uint32_t) id * 2654435761u) >> (32 - HL);
-    for (;;) {
-        const uint32_t h = s_cnt[HB + sl];
-        if (h == (uint32_t) id) return (int) sl;
-        if (h == 0xffffffffu) return -1;
-        sl = (sl + 1u) & ((1u << HL) - 1u);
-    }
-}
-
-// Counts one history id into its survivor's slot (ids outside [lo, hi) and ids that did not survive are skipped).
-template <int HB, int HL>
-__device__ __forceinline__ void hash_count(int id, int lo, int hi) {
-    if ((uint32_t) id - (uint32_t) lo >= (uint32_t) (hi - lo)) return;
-    const int sl = hash_find<HB, HL>(id);
-    if (sl >= 0) atomicAdd(&s_cnt[HB + (1 << HL) + sl], 1u);
-}
-
 // The history counts of the four ids lo + 4*(i*WG + tid) + e from the table over [tlo, ...); 0 past hi (unless
 // INR: every id is below hi).
 template <int WG, bool C16, bool INR>
@@ -478,6 +440,9 @@ __device__ __forceinline__ void group_counts(uint32_t (&c)[4], int i, int lo, in
         if (!INR && id0 + e >= hi) c[e] = 0u;
 }
 
+// Applies the table's counts to the four logits of group i this thread holds (ids lo + 4*(i*WG + tid) + e).
+// Nearly every wave-wide group holds some history id, so the penalty is computed for all four logits and
+// selected where the count is nonzero (no divergent branches). INR: every id is below hi.
 template <int WG, int EPT, bool C16, bool INR>
 __device__ __forceinline__ void apply_group(float (&v)[EPT], int i, int lo, int hi, int tlo, const SamplingParams& p) {
     uint32_t c[4];
@@ -908,6 +873,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     float v[EPT];
     RawHistory rh;
     bool wide = false;
+    // Penalties that never raise a logit (rep >= 1, presence >= 0, frequency >= 0: penalized <= raw for every
+    // id) are applied lazily. Greedy rows penalize a history logit when its raw value beats the running maximum;
+    // top-k rows scan raw logits and penalize afterwards only the lane maxima and the logits that pass the bound.
+    const bool late = !GREEDY && PENALIZE && a.p.lazy;
     load_groups<FULL, WG, EPT, 0, Q1>(v, vec, seg_rsrc, L, lb, hi);
     if (PENALIZE) {
         int4 hq[HR];
@@ -929,21 +898,20 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         const int extra = (a.extra_a ? PENDING_CAP : 0) + (a.extra_b ? VERIFY_MAX_ROWS : 0);
         wide = C16 && (a.count_wide != 0 || (rh.s1 - rh.s0) + extra >= 65536);
         if (!wide) cnt_zero<WG>(C16 ? (hi - lb + 1) / 2 : hi - lb);
-        // (the barrier comes before the middle batch: every wave reaches it having issued few loads; a wave
-        // whose loads wait for issue slots would hold the others here)
+        // (the barrier comes before the rest of the segment: every wave reaches it having issued few loads; a
+        // wave whose loads wait for issue slots would hold the others here)
         __syncthreads();  // table zeroed
         load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
         if (!wide) {
             count_history<WG, C16, true>(a, row, lb, hi, hq, rh);
-            __syncthreads();  // table complete (before the last batch, for the same reason)
+            // (before the last batch, for the same reason; late counts are first read after the scan)
+            if (!late) __syncthreads();  // table complete
+            else __builtin_amdgcn_sched_barrier(0);  // (the last batch stays after the count)
         }
     }
     load_groups<FULL, WG, EPT, Q3, NV>(v, vec, seg_rsrc, L, lb, hi);
     // with penalties (16-bit or narrow tables) the counts are applied group by group as the logits are first
-    // used, below; wide counts are applied here, half a segment at a time
-    // Penalties that never raise a logit (rep >= 1, presence >= 0, frequency >= 0: penalized <= raw for every
-    // id) are applied lazily: history ids are left out of the bounds, and only a history logit whose raw value
-    // passes a bound is penalized and tested again. Otherwise every count is applied as the logits arrive.
+    // used (or lazily), below; wide counts are applied here, half a segment at a time
     const bool pen_now = PENALIZE && !wide && !a.p.lazy;
     const bool pen_lazy = PENALIZE && !wide && a.p.lazy;
     if (PENALIZE && wide) {
@@ -1006,32 +974,35 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // (canonicalized values: signaling NaNs quieted, so max ignores a NaN and med3 keeps m2, and every NaN fails
         // the filter's compares; med3(m1, m2, x) = max(m2, min(m1, x)) for m1 >= m2)
         float m1 = -INFINITY, m2 = -INFINITY;
-        float hm = -INFINITY;  // lazy: largest raw logit of a history id
-        int s1 = 0;            // slot 4*i+e of m1 (its first occurrence)
-        // lazy: the counts of group i+1 are read while group i is worked on
-        uint32_t cn[4] = {0u, 0u, 0u, 0u};
-        if (pen_lazy) group_counts<WG, C16, FULL>(cn, 0, lb, hi, lb, m2);
+        int s1 = 0;  // slot 4*i+e of m1 (its first occurrence)
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             if (pen_now) apply_group<WG, EPT, C16, FULL>(v, i, lb, hi, lb, a.p);
-            const uint32_t c[4] = {cn[0], cn[1], cn[2], cn[3]};
-            if (pen_lazy && i + 1 < NV) group_counts<WG, C16, FULL>(cn, i + 1, lb, hi, lb, m2);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float x = __builtin_canonicalizef(v[4 * i + e]);
                 v[4 * i + e] = x;
-                const float xb = c[e] != 0u ? -INFINITY : x;  // lazy: history ids stay out of the bound
-                if (pen_lazy) hm = __builtin_fmaxf(hm, c[e] != 0u ? x : -INFINITY);
-                s1 = xb > m1 ? 4 * i + e : s1;
-                asm volatile("" : "+v"(s1));  // kept as a register update (not deferred per-slot compares)
-                m2 = __builtin_amdgcn_fmed3f(m1, m2, xb);
-                m1 = __builtin_fmaxf(m1, xb);
+                s1 = x > m1 ? 4 * i + e : s1;
+                m2 = __builtin_amdgcn_fmed3f(m1, m2, x);
+                m1 = __builtin_fmaxf(m1, x);
+                // (kept as register updates: otherwise the compiler defers them and holds every partial maximum)
+                asm volatile("" : "+v"(s1), "+v"(m2));
+            }
+        }
+        // lazy: the lane's contribution to the bound is its maximum's penalized value (a logit of the lane
+        // that reaches it); m2 stays raw, an upper bound of every other penalized logit of the lane
+        if (pen_lazy) {
+            __syncthreads();  // table complete
+            if (m1 > -INFINITY) {
+                const int off = 4 * ((s1 >> 2) * WG + tid) + (s1 & 3);
+                const uint32_t c = C16 ? (s_cnt[off >> 1] >> ((off & 1) << 4)) & 0xffffu : s_cnt[off];
+                if (c != 0u) m1 = penalize(m1, c, a.p);
             }
         }
         uint32_t gl;
         if constexpr (NW == 4) {
             const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
-            const uint32_t l2 = sort32<false>(ord_f32(m2), lane);
+            const uint32_t l2 = sort32<false>(pen_lazy ? 0u : ord_f32(m2), lane);  // (lazy: raw m2 has no id)
             s_mx<NW>[wave][lane] = bitonic_stage32<64, true>(max(l1, l2), lane);
             __syncthreads();
             gl = s_mx<NW>[0][lane];
@@ -1062,11 +1033,11 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         const uint32_t q = NW == 4 ? (uint32_t) rdlanei((int) gl, k - 1) : gl;  // all lanes active
         const float t_f = fmaxf(floor32(q), floor64(t_row));
 
-        // ---- filter: survivors go to the wave's LDS region. A lane whose second largest logit (and, lazily, every
-        // history logit) is below the bound holds at most one survivor, its maximum at slot s1, offered directly;
-        // the other lanes compare every logit.
+        // ---- filter: survivors go to the wave's LDS region. A lane whose second largest (raw) logit is below the
+        // bound holds at most one survivor, its maximum at slot s1 (penalized, lazily), offered directly; the other
+        // lanes' logits are tested one by one (lazily penalized when their raw value passes).
         WaveCollect<NW> w;
-        const bool multi = (pen_lazy ? __builtin_fmaxf(m2, hm) : m2) >= t_f;
+        const bool multi = m2 >= t_f;
         {
             const int slot = 4 * ((s1 >> 2) * WG + tid) + (s1 & 3);
             const bool pass = !multi && m1 >= t_f && slot >= skip;
