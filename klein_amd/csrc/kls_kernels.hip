@@ -869,7 +869,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // never held at once.
     const __amdgpu_buffer_rsrc_t seg_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(L + lb), (short) 0, SEG * 4, kRawBufferFlags);
-    constexpr int Q1 = PENALIZE ? (NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : NV, Q3 = PENALIZE ? NV - NV / 4 : NV;
+    constexpr int Q1 = PENALIZE ? (NV >= 16 ? 4 : NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : NV, Q3 = PENALIZE ? NV - NV / 4 : NV;
     float v[EPT];
     RawHistory rh;
     bool wide = false;
@@ -1112,14 +1112,22 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         return;
     }
 
-    // Few segments: wave 0 merges the lists one after another (each is sorted, the first k entries valid).
+    // Few segments: wave 0 merges the lists one after another (each is sorted, the first k entries valid). Every
+    // lane loads from every list slot (clamped to the row's lists; entries past k are stale and zeroed), so the
+    // loads are issued together, with the row's uniform.
     if (a.segs <= 8) {
         if (wave != 0) return;
+        const double u_row = a.u[row];
         uint64_t lk[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const int l = s == 0 ? lane : 63 - lane;  // lists after the first are read reversed (ascending)
-            lk[s] = (s < a.segs && l < k) ? load_dev(&cand[(int64_t) s * KCAP + l]) : 0ull;
+            lk[s] = load_dev(&cand[(int64_t) min(s, a.segs - 1) * KCAP + l]);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int l = s == 0 ? lane : 63 - lane;
+            lk[s] = (s < a.segs && l < k) ? lk[s] : 0ull;
         }
         uint64_t lst = lk[0];
 #pragma unroll
@@ -1127,7 +1135,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             if (s < a.segs) lst = merge64(lst, lk[s], lane);
         const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
         if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
-        const int tok = sample_tail(lst, kk, a.p, a.u[row], lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
+        const int tok = sample_tail(lst, kk, a.p, u_row, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
                                     a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
         if (lane == 0) publish(a, row, tok);
         return;
@@ -1143,14 +1151,17 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     const int nH = min(a.segs * J, WG);
     const bool one = nH <= 64;
     const int h = one ? (wave == 0 ? lane : WG) : lane * NW + wave;
-    const uint64_t hv = h < nH ? load_dev(&cand[(int64_t) (h / J) * KCAP + h % J]) : 0ull;
+    // (loads clamped to the row's lists and issued together; what is out of range is zeroed after)
+    const double u_row = a.u[row];
+    const int hc = min(h, nH - 1);
+    uint64_t hv = load_dev(&cand[(int64_t) (hc / J) * KCAP + hc % J]);
     const bool inreg = a.segs <= NW * RB;
     uint64_t key[RB];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        const int s = wave + NW * r;
-        key[r] = (inreg && s < a.segs && lane < k) ? load_dev(&cand[(int64_t) s * KCAP + lane]) : 0ull;
-    }
+    for (int r = 0; r < RB; ++r) key[r] = load_dev(&cand[(int64_t) min(wave + NW * r, a.segs - 1) * KCAP + lane]);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) key[r] = (inreg && wave + NW * r < a.segs && lane < k) ? key[r] : 0ull;
+    hv = h < nH ? hv : 0ull;
     const uint32_t sv = sort32<true>((uint32_t) (hv >> 32), lane);
     const uint32_t qw = (uint32_t) rdlanei((int) sv, (one ? k : (k + NW - 1) / NW) - 1);  // all lanes active
     if (lane == 0) s_q<NW>[wave] = (one && wave != 0) ? 0xffffffffu : qw;
@@ -1182,7 +1193,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     if (wave != 0) return;
     const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
     if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
-    const int tok = sample_tail(lst, kk, a.p, a.u[row], lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
+    const int tok = sample_tail(lst, kk, a.p, u_row, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
                                 a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
     if (lane == 0) publish(a, row, tok);
 }
