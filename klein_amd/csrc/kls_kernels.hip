@@ -42,6 +42,7 @@ template <int NW> __shared__ int s_n[NW];
 template <int NW> __shared__ uint32_t s_mx[NW][64];    // per-wave sorted lane maxima
 template <int NW> __shared__ uint32_t s_mx4[4][64];    // their merges in groups of four waves
 __shared__ int s_last;
+__shared__ int s_counted;  // waves done counting the history (lazy top-k rows)
 
 
 // ---------------------------------------------------------------------------------------------------------
@@ -565,10 +566,8 @@ __device__ __forceinline__ uint64_t select_regions(const int (&cnt)[NW], int tot
         __syncthreads();
         return merge_lists<NW>(NW, lane, wave);
     }
-    uint64_t lst = 0ull;
-    if (wave < nc) {
-        // chunk `wave` of the concatenated regions: find the region of entry j, then one read
-        const int j = 64 * wave + lane;
+    // entry j of the concatenated regions: find its region, then one read
+    auto entry = [&](int j) {
         int r = 0, base = 0, end = cnt[0];
 #pragma unroll
         for (int q = 1; q < NW; ++q) {
@@ -577,9 +576,10 @@ __device__ __forceinline__ uint64_t select_regions(const int (&cnt)[NW], int tot
             base = past ? end : base;
             end += cnt[q];
         }
-        const uint64_t key = j < total ? s_cand<NW>[r][j - base] : 0ull;
-        lst = sort64<true>(key, lane);
-    }
+        return j < total ? s_cand<NW>[r][j - base] : 0ull;
+    };
+    uint64_t lst = 0ull;
+    if (wave < nc) lst = sort64<true>(entry(64 * wave + lane), lane);  // chunk `wave`
     if (nc <= 1) return wave == 0 ? lst : 0ull;
     if (wave < nc) s_list<NW>[wave][lane] = lst;
     __syncthreads();
@@ -877,14 +877,21 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // id) are applied lazily. Greedy rows penalize a history logit when its raw value beats the running maximum;
     // top-k rows scan raw logits and penalize afterwards only the lane maxima and the logits that pass the bound.
     const bool late = !GREEDY && PENALIZE && a.p.lazy;
+    // (the row's history bounds are read first: their latency overlaps the first batch and the table clearing)
+    if (PENALIZE && a.hist_off) {
+        rh.s0 = max(a.hist_off[row], 0);
+        rh.s1 = max(a.hist_off[row + 1], rh.s0);
+    }
     load_groups<FULL, WG, EPT, 0, Q1>(v, vec, seg_rsrc, L, lb, hi);
     if (PENALIZE) {
+        // cleared whatever the table's width turns out to be (wide tables are cleared again per half)
+        cnt_zero<WG>(C16 ? (hi - lb + 1) / 2 : hi - lb);
+        if (tid == 0) s_counted = 0;  // (ordered before every increment by the barrier below)
+        __builtin_amdgcn_sched_barrier(0);
         int4 hq[HR];
 #pragma unroll
         for (int r = 0; r < HR; ++r) hq[r] = make_int4(-1, -1, -1, -1);
         if (a.hist_off) {
-            rh.s0 = max(a.hist_off[row], 0);
-            rh.s1 = max(a.hist_off[row + 1], rh.s0);
             const bool hv = (reinterpret_cast<uintptr_t>(a.hist_ids) & 15u) == 0;
             rh.b0 = hv ? min(rh.s1, (rh.s0 + 3) & ~3) : rh.s1;
             rh.b1 = hv ? max(rh.b0, rh.s1 & ~3) : rh.s1;
@@ -897,16 +904,20 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // counts reach 65536 only with that many history ids in the row (extras included)
         const int extra = (a.extra_a ? PENDING_CAP : 0) + (a.extra_b ? VERIFY_MAX_ROWS : 0);
         wide = C16 && (a.count_wide != 0 || (rh.s1 - rh.s0) + extra >= 65536);
-        if (!wide) cnt_zero<WG>(C16 ? (hi - lb + 1) / 2 : hi - lb);
         // (the barrier comes before the rest of the segment: every wave reaches it having issued few loads; a
         // wave whose loads wait for issue slots would hold the others here)
         __syncthreads();  // table zeroed
         load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
         if (!wide) {
             count_history<WG, C16, true>(a, row, lb, hi, hq, rh);
-            // (before the last batch, for the same reason; late counts are first read after the scan)
-            if (!late) __syncthreads();  // table complete
-            else __builtin_amdgcn_sched_barrier(0);  // (the last batch stays after the count)
+            // (before the last batch, for the same reason; late counts are first read after the scan, once every
+            // wave has announced its count: LDS operations of a wave complete in order)
+            if (!late) {
+                __syncthreads();  // table complete
+            } else {
+                if (lane == 0) __hip_atomic_fetch_add(&s_counted, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __builtin_amdgcn_sched_barrier(0);  // (the last batch stays after the count)
+            }
         }
     }
     load_groups<FULL, WG, EPT, Q3, NV>(v, vec, seg_rsrc, L, lb, hi);
@@ -992,7 +1003,12 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // lazy: the lane's contribution to the bound is its maximum's penalized value (a logit of the lane
         // that reaches it); m2 stays raw, an upper bound of every other penalized logit of the lane
         if (pen_lazy) {
-            __syncthreads();  // table complete
+            // table complete: every wave has counted (each does so right after issuing its loads, whatever the
+            // others do, so the wait ends; the bound on it is a guard only)
+            for (int spin = 0; spin < (1 << 20); ++spin) {
+                if (__hip_atomic_load(&s_counted, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
             if (m1 > -INFINITY) {
                 const int off = 4 * ((s1 >> 2) * WG + tid) + (s1 & 3);
                 const uint32_t c = C16 ? (s_cnt[off >> 1] >> ((off & 1) << 4)) & 0xffffu : s_cnt[off];
