@@ -266,6 +266,16 @@ __device__ __forceinline__ uint32_t merge32(uint32_t a, uint32_t b, int lane) {
 }
 
 
+// Inserts the wave-uniform key x into the descending list held one key per lane (keys distinct; the smallest
+// falls off): lanes below x's position keep theirs, the rest shift down one lane (DPP wave_shr:1).
+__device__ __forceinline__ uint64_t insert64(uint64_t lst, uint64_t x, int lane) {
+    const int pos = __popcll(ballot(lst > x));
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) lst, 0x138, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) (lst >> 32), 0x138, 0xf, 0xf, false);
+    const uint64_t sh = ((uint64_t) hi << 32) | lo;
+    return lane < pos ? lst : (lane == pos ? x : sh);
+}
+
 __device__ __forceinline__ uint64_t wave_max64(uint64_t x, int lane) {
     x = max64(x, xor_lane64<32>(x, lane));
     x = max64(x, xor_lane64<16>(x, lane));
@@ -317,6 +327,40 @@ __device__ __forceinline__ float expf_glibc(float x) {
     y = __builtin_fma(z, r2, y);
     y = __dmul_rn(y, s);
     return __double2float_rn(y);
+}
+
+// expf_glibc with the table in registers: lane l of `tab` holds kExp2Tab[l & 31], read across lanes
+// (ds_bpermute), so every lane of the wave must call it; the special cases are selected after.
+__device__ __forceinline__ float expf_glibc_tab(float x, uint64_t tab) {
+    const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double) x;
+    double kd = __builtin_fma(inv_ln2_32, xd, shift);
+    const uint64_t ki = (uint64_t) __double_as_longlong(kd);
+    kd = __dsub_rn(kd, shift);
+    const double r = __builtin_fma(inv_ln2_32, xd, -kd);
+    const int src = (int) (ki & 31u) << 2;
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_ds_bpermute(src, (int) (uint32_t) tab);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_ds_bpermute(src, (int) (uint32_t) (tab >> 32));
+    const uint64_t t = (((uint64_t) hi << 32) | lo) + (ki << 47);
+    const double s = __longlong_as_double((long long) t);
+    const double z = __builtin_fma(c0, r, c1);
+    const double r2 = __dmul_rn(r, r);
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = __dmul_rn(y, s);
+    float res = __double2float_rn(y);
+    const uint32_t ux = __float_as_uint(x);
+    if (((ux >> 20) & 0x7ffu) >= 0x42bu) {  // |x| >= 88 or nan: as expf_glibc
+        if (ux == 0xff800000u) res = 0.0f;
+        else if (((ux >> 20) & 0x7ffu) >= 0x7f8u) res = x + x;
+        else if (x > 0x1.62e42ep6f) res = __uint_as_float(0x7f800000u);
+        else if (x < -0x1.9fe368p6f) res = 0.0f;
+    }
+    return res;
 }
 
 // Penalty of src/sampler.cpp:24-25 for an id seen `c` > 0 times: repetition first (l > 0 ? l / rep : l * rep),
@@ -578,6 +622,15 @@ __device__ __forceinline__ uint64_t select_regions(const int (&cnt)[NW], int tot
         }
         return j < total ? s_cand<NW>[r][j - base] : 0ull;
     };
+    const int extra = total - 64;
+    if (extra > 0 && extra <= 16) {
+        // a few keys past one chunk: wave 0 sorts the first 64 and inserts the others one at a time
+        if (wave != 0) return 0ull;
+        uint64_t lst = sort64<true>(entry(lane), lane);
+        const uint64_t ex = entry(64 + lane);
+        for (int t = 0; t < extra; ++t) lst = insert64(lst, rdlane64(ex, t), lane);
+        return lst;
+    }
     uint64_t lst = 0ull;
     if (wave < nc) lst = sort64<true>(entry(64 * wave + lane), lane);  // chunk `wave`
     if (nc <= 1) return wave == 0 ? lst : 0ull;
@@ -737,8 +790,9 @@ __device__ __forceinline__ double chain_draw(double r, float p, int n, int lane)
     return mine;
 }
 
-__device__ int sample_tail(uint64_t lst, int kk, const SamplingParams p, double u, int lane, float* dbg_probs,
-                           int32_t* dbg_meta) {
+// exp_tab: lane l holds kExp2Tab[l & 31] (loaded ahead by the caller).
+__device__ int sample_tail(uint64_t lst, int kk, const SamplingParams p, double u, uint64_t exp_tab, int lane,
+                           float* dbg_probs, int32_t* dbg_meta) {
     if (kk == 0) return 0;
     const bool act = lane < kk;
     const float v = act ? unord_f32((uint32_t) (lst >> 32)) : 0.0f;
@@ -746,7 +800,8 @@ __device__ int sample_tail(uint64_t lst, int kk, const SamplingParams p, double 
     // softmax with temperature (:53-60)
     const float maxl = rdlanef(v, 0);
     const float x = __fdiv_rn(__fsub_rn(v, maxl), p.temperature);
-    const float e = act ? expf_glibc(x) : 0.0f;
+    const float ex = expf_glibc_tab(x, exp_tab);  // (all lanes)
+    const float e = act ? ex : 0.0f;
     const bool exact_e = ballot(act && e < 0x1p-23f) == 0ull;
     const double sum = exact_e ? wave_sum_f64((double) e, lane) : chain_sum(e, kk);
     const float pr = act ? __double2float_rn(__ddiv_rn((double) e, sum)) : 0.0f;
@@ -1100,7 +1155,57 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // ---- the last workgroup of the row merges the segment results. Hand-off: the segment results above were
     // written (by wave 0, which also takes the ticket) with device-scope stores; the wave waits for them to be
     // acknowledged before the ticket increment, and the last workgroup reads them with device-scope loads after
-    // its increment returned.
+    // its increment returned. With few segments wave 0 does all of it alone (no barrier).
+    const uint64_t* cand = a.seg_cand + (int64_t) row * a.segs * KCAP;
+    if (GREEDY ? a.segs <= 64 : a.segs <= 8) {
+        if (wave != 0) return;
+        wait_stores();
+        uint32_t prev = 0u;
+        if (lane == 0) prev = atomicAdd(&a.row_ticket[row], 1u);
+        if ((uint32_t) rdlanei((int) prev, 0) != (uint32_t) (a.segs - 1)) return;
+        if (GREEDY) {
+            uint64_t m = load_dev(&cand[(int64_t) min(lane, a.segs - 1) * KCAP]);
+            m = wave_max64(lane < a.segs ? m : 0ull, lane);
+            if (lane == 0) {
+                if (a.dbg_meta) {
+                    a.dbg_meta[row * 2] = 0;
+                    a.dbg_meta[row * 2 + 1] = 0;
+                }
+                publish(a, row, m ? key_id(m) : 0);  // all -inf / NaN: the reference returns id 0
+            }
+            return;
+        }
+        // The lists (each sorted, the first k entries valid) are merged as a tree: pairs, then pairs of pairs.
+        // Every lane loads from every list slot (clamped to the row's lists; entries past k are stale and zeroed),
+        // so the loads are issued together, with the row's uniform. Odd lists are read reversed (ascending).
+        const double u_row = a.u[row];
+        const uint64_t exp_tab = kExp2Tab[lane & 31];
+        uint64_t lk[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) lk[s] = load_dev(&cand[(int64_t) min(s, a.segs - 1) * KCAP + ((s & 1) ? 63 - lane : lane)]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) lk[s] = (s < a.segs && ((s & 1) ? 63 - lane : lane) < k) ? lk[s] : 0ull;
+        // (merged descending where the result is a left operand, ascending where it is a right one)
+        uint64_t lst = a.segs > 1 ? bitonic_stage<64, true>(max64(lk[0], lk[1]), lane) : lk[0];
+        if (a.segs > 2) {
+            const uint64_t m23 = bitonic_stage<64, false>(max64(lk[2], lk[3]), lane);
+            if (a.segs > 4) {
+                const uint64_t m45 = bitonic_stage<64, true>(max64(lk[4], lk[5]), lane);
+                const uint64_t m67 = bitonic_stage<64, false>(max64(lk[6], lk[7]), lane);
+                const uint64_t m0123 = bitonic_stage<64, true>(max64(lst, m23), lane);
+                const uint64_t m4567 = bitonic_stage<64, false>(max64(m45, m67), lane);
+                lst = bitonic_stage<64, true>(max64(m0123, m4567), lane);
+            } else {
+                lst = bitonic_stage<64, true>(max64(lst, m23), lane);
+            }
+        }
+        const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
+        if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
+        const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
+                                    a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
+        if (lane == 0) publish(a, row, tok);
+        return;
+    }
     __syncthreads();
     if (tid == 0) {
         wait_stores();
@@ -1109,7 +1214,6 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
-    const uint64_t* cand = a.seg_cand + (int64_t) row * a.segs * KCAP;
 
     if (GREEDY) {
         uint64_t m = 0ull;
@@ -1128,35 +1232,6 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         return;
     }
 
-    // Few segments: wave 0 merges the lists one after another (each is sorted, the first k entries valid). Every
-    // lane loads from every list slot (clamped to the row's lists; entries past k are stale and zeroed), so the
-    // loads are issued together, with the row's uniform.
-    if (a.segs <= 8) {
-        if (wave != 0) return;
-        const double u_row = a.u[row];
-        uint64_t lk[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const int l = s == 0 ? lane : 63 - lane;  // lists after the first are read reversed (ascending)
-            lk[s] = load_dev(&cand[(int64_t) min(s, a.segs - 1) * KCAP + l]);
-        }
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const int l = s == 0 ? lane : 63 - lane;
-            lk[s] = (s < a.segs && l < k) ? lk[s] : 0ull;
-        }
-        uint64_t lst = lk[0];
-#pragma unroll
-        for (int s = 1; s < 8; ++s)
-            if (s < a.segs) lst = merge64(lst, lk[s], lane);
-        const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
-        if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
-        const int tok = sample_tail(lst, kk, a.p, u_row, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
-                                    a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
-        if (lane == 0) publish(a, row, tok);
-        return;
-    }
-
     // Lower bound of the row's k-th value from the heads of the segment lists: H = the first J = ceil(k/segs)
     // entries of every list (J*segs >= k distinct logits). With |H| <= 64 the bound is the k-th largest value in H;
     // otherwise H is dealt round-robin to the waves and the bound is the smallest of the waves'
@@ -1169,6 +1244,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     const int h = one ? (wave == 0 ? lane : WG) : lane * NW + wave;
     // (loads clamped to the row's lists and issued together; what is out of range is zeroed after)
     const double u_row = a.u[row];
+    const uint64_t exp_tab = kExp2Tab[lane & 31];
     const int hc = min(h, nH - 1);
     uint64_t hv = load_dev(&cand[(int64_t) (hc / J) * KCAP + hc % J]);
     const bool inreg = a.segs <= NW * RB;
@@ -1209,7 +1285,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     if (wave != 0) return;
     const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
     if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
-    const int tok = sample_tail(lst, kk, a.p, u_row, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
+    const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
                                 a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
     if (lane == 0) publish(a, row, tok);
 }
