@@ -50,7 +50,9 @@ typedef void* kls_stream;
 
 /* Replaces Sampler::Sampler (src/sampler.cpp:11). Binds the current HIP device, allocates every buffer the
  * handle will use (no allocation happens in the calls below), and starts with an empty token history.
- * max_rows bounds the rows of kls_verify and kls_sample_batch. */
+ * max_rows bounds the rows of kls_verify and kls_sample_batch. A top-k above 64 (or no limit) takes a slower
+ * path that keys and sorts every logit of a row (2 x 8 bytes per logit per row of device memory); it needs
+ * n_vocab * max_rows below 2^32 (KLS_ERR_UNSUPPORTED otherwise). */
 int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* out);
 
 int kls_destroy(kls_handle h);

@@ -73,6 +73,10 @@ struct kls_sampler {
     float* d_rows_buf = nullptr;  // host logits are copied here
     int max_segs = 0;
 
+    // wide top-k (k above KCAP): key buffers and the sort's scratch
+    bool wide = false;
+    WideArgs w{};
+
     // pinned host blocks
     CallBlock* call = nullptr;    // host view
     ResultBlock* res = nullptr;
@@ -228,7 +232,10 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
     if (st) return st;
     h->call->seq = ++h->seq;
     const RowsArgs a = step_args(h, dl, rows, verify);
-    if (verify) {
+    if (h->wide) {
+        // (several kernels and a library sort: launched directly, not captured)
+        KLS_HIP(launch_wide(a, h->w, h->penalize, s));
+    } else if (verify) {
         if (!h->g_valid || h->g_logits != dl || h->g_rows != rows) {
             // (a stale graph is replaced whether or not its teardown reports an error)
             if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
@@ -319,7 +326,8 @@ int kls_destroy(kls_handle h) {
     if (h->graph) (void) hipGraphDestroy(h->graph);
     void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_seg_cand,
                    h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_dbg_keys,
-                   h->d_dbg_probs, h->d_dbg_meta, h->d_rows_buf};
+                   h->d_dbg_probs, h->d_dbg_meta, h->d_rows_buf, h->w.keys,
+                   h->w.sorted, h->w.sort_tmp};
     for (void* p : dev)
         if (p) (void) hipFree(p);
     if (h->h_stage) (void) hipHostFree(h->h_stage);
@@ -336,8 +344,12 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     if (n_vocab <= 0) return fail(KLS_ERR_INVALID_ARG, "n_vocab must be positive");
     if (max_rows < 1) return fail(KLS_ERR_INVALID_ARG, "max_rows must be positive");
     const int k = (params->top_k > 0 && params->top_k < n_vocab) ? params->top_k : n_vocab;
-    if (params->temperature > 0.0f && k > KCAP)
-        return fail(KLS_ERR_UNSUPPORTED, "top-k above 64 (including no limit) is not implemented");
+    // k above KCAP (or no limit) takes the wide path, whose keys hold an id and a row index in 32 bits
+    const bool wide = params->temperature > 0.0f && k > KCAP;
+    int row_bits = 0;
+    while ((1ll << row_bits) < (long long) max_rows) ++row_bits;
+    if (wide && wide_id_bits(n_vocab) + row_bits > 32)
+        return fail(KLS_ERR_UNSUPPORTED, "top-k above 64 with this many rows of this vocabulary");
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
         (void) hipGetLastError();
@@ -349,6 +361,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     h->max_rows = max_rows;
     h->k = k;
     h->greedy = params->temperature <= 0.0f;
+    h->wide = wide;
     h->penalize = params->presence_penalty != 0.0f || params->frequency_penalty != 0.0f ||
                   params->repetition_penalty != 1.0f;
     h->sp = SamplingParams{params->temperature, params->top_p, params->min_p, params->presence_penalty,
@@ -390,6 +403,16 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     ALLOC(h->d_dbg_probs, sizeof(float) * R * KCAP);
     ALLOC(h->d_dbg_meta, sizeof(int32_t) * R * 2);
     ALLOC(h->d_rows_buf, sizeof(float) * R * n_vocab);
+    if (wide) {
+        h->w.k = k;
+        h->w.id_bits = wide_id_bits(n_vocab);
+        ALLOC(h->w.keys, sizeof(uint64_t) * R * n_vocab);
+        ALLOC(h->w.sorted, sizeof(uint64_t) * R * n_vocab);
+        if ((e = sort_keys_desc(nullptr, &h->w.sort_tmp_bytes, h->w.keys, h->w.sorted, R * n_vocab, 64, h->stream)) !=
+            hipSuccess)
+            return oom("sort scratch size", e);
+        ALLOC(h->w.sort_tmp, h->w.sort_tmp_bytes);
+    }
 #undef ALLOC
     if ((e = hipHostMalloc((void**) &h->h_stage, sizeof(int32_t) * (2 * (size_t) n_vocab + h->n_buckets + 1),
                            hipHostMallocDefault)) != hipSuccess)
@@ -499,7 +522,10 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
     }
     a.u = d_u;
     a.out_tokens = d_out_tokens;
-    KLS_HIP(launch_rows(a, h->greedy, pen, s));
+    if (h->wide)
+        KLS_HIP(launch_wide(a, h->w, pen, s));
+    else
+        KLS_HIP(launch_rows(a, h->greedy, pen, s));
     return KLS_OK;
 }
 

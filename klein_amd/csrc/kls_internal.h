@@ -97,10 +97,33 @@ struct RowsArgs {
 };
 
 
+// Wide top-k (k above KCAP, up to no limit; src/sampler.cpp:42-51): every logit of a row becomes one 64-bit key
+//   (row field << (32 + id_bits)) | (order-preserving image of the (penalized) value << id_bits) | (~id & id mask)
+// with row field = n_rows - 1 - row, so one descending device-wide sort of all rows' keys leaves each row's keys
+// contiguous, value-descending and, on equal values, id-ascending (the fast path's order). NaN maps to the
+// value image 0, after every number. The sorted keys then go through the O(k) tail in reference order.
+struct WideArgs {
+    uint64_t* keys;       // [n_rows * V]
+    uint64_t* sorted;     // [n_rows * V]
+    void* sort_tmp;       // device sort scratch
+    size_t sort_tmp_bytes;
+    int32_t k;            // KCAP < k <= V
+    int32_t id_bits;      // ids are below 1 << id_bits
+};
+
 // Launchers (kls_kernels.hip). Return hipSuccess or the launch error.
 hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_t s);
 int rows_grid(const RowsArgs& a);  // workgroups launch_rows starts
 hipError_t prepare_rows_kernels();  // once per device: LDS limits of the kernels with large count tables
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s);
+// Wide top-k: keys (with penalties from the history in `a`), the sort, the tail (tokens published as
+// launch_rows does).
+hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipStream_t s);
+int wide_id_bits(int V);  // key bits the ids of a V-entry vocabulary take
+
+// Descending device-wide sort of n 64-bit keys on bits [0, end_bit) (kls_sort.hip). With tmp == nullptr, sets
+// *bytes to the scratch size.
+hipError_t sort_keys_desc(void* tmp, size_t* bytes, const uint64_t* in, uint64_t* out, size_t n, int end_bit,
+                          hipStream_t s);
 
 }  // namespace kls

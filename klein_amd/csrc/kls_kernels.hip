@@ -1295,6 +1295,157 @@ __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
     if (i < n) out[i] = expf_glibc(__uint_as_float(lo + (uint32_t) i));
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Wide top-k (k above 64, up to no limit; src/sampler.cpp:42-51): keys of every logit, one device-wide sort,
+// then the tail over the sorted keys.
+
+constexpr int WIDE_WG = 256;
+constexpr int WIDE_SEG = 4096;  // ids per keys workgroup (32-bit history counts: 16 KB of LDS)
+
+// Keys of ids [lo, hi) of one row (workgroup = (row, segment)), every history count applied to its logit.
+template <bool PENALIZE>
+__global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs w) {
+    const int segs = (a.V + WIDE_SEG - 1) / WIDE_SEG;
+    const int row = (int) blockIdx.x / segs, seg = (int) blockIdx.x - row * segs;
+    const int lo = seg * WIDE_SEG, hi = min(a.V, lo + WIDE_SEG);
+    const float* __restrict__ L = a.logits + (int64_t) row * a.row_stride;
+    if (PENALIZE) {
+        RawHistory rh;
+        if (a.hist_off) {
+            rh.s0 = max(a.hist_off[row], 0);
+            rh.s1 = max(a.hist_off[row + 1], rh.s0);
+            const bool hv = (reinterpret_cast<uintptr_t>(a.hist_ids) & 15u) == 0;
+            rh.b0 = hv ? min(rh.s1, (rh.s0 + 3) & ~3) : rh.s1;
+            rh.b1 = hv ? max(rh.b0, rh.s1 & ~3) : rh.s1;
+        }
+        const int4 none[HR] = {};
+        cnt_zero<WIDE_WG>(hi - lo);
+        __syncthreads();
+        count_history<WIDE_WG, false, false>(a, row, lo, hi, none, rh);
+        __syncthreads();
+    }
+    const int ib = w.id_bits;
+    const uint64_t rf = (uint64_t) (a.n_rows - 1 - row) << (32 + ib);
+    const uint32_t idm = (1u << ib) - 1u;
+    uint64_t* __restrict__ out = w.keys + (int64_t) row * a.V;
+    for (int id = lo + (int) threadIdx.x; id < hi; id += WIDE_WG) {
+        float x = L[id];
+        if (PENALIZE) {
+            const uint32_t c = s_cnt[id - lo];
+            if (c != 0u) x = penalize(x, c, a.p);
+        }
+        out[id] = rf | ((uint64_t) ord_f32(x) << ib) | (uint64_t) (~(uint32_t) id & idm);
+    }
+}
+
+// The tail of src/sampler.cpp:53-88 over a row's sorted keys, one wave per row: candidate i is the row's i-th
+// key (value descending, id ascending), numbers only (NaN keys sort last and are left out). Every sum is the
+// reference's sequential double chain, one addition per candidate in candidate order; each pass walks the
+// candidates in chunks of 64 (lane j holding candidate c + j) and recomputes e_i and p_i as it goes.
+__global__ __launch_bounds__(64) void wide_tail_kernel(RowsArgs a, WideArgs w) {
+    const int row = (int) blockIdx.x, lane = (int) threadIdx.x;
+    const int ib = w.id_bits, k = w.k;
+    const uint64_t vmask = (1ull << (32 + ib)) - 1ull;
+    const uint32_t idm = (1u << ib) - 1u;
+    const uint64_t* __restrict__ K = w.sorted + (int64_t) row * a.V;
+    const SamplingParams p = a.p;
+    const uint64_t tab = kExp2Tab[lane & 31];
+    const double u_row = a.u[row];
+    auto img = [&](int i, int lim) { return i < lim ? (uint32_t) ((K[i] & vmask) >> ib) : 0u; };  // 0: none
+    const uint32_t o0 = img(0, 1);
+    if (o0 == 0u) {  // no number in the row: the fast path's empty candidate list
+        if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = 0ull;
+        if (lane == 0) {
+            if (a.dbg_meta) {
+                a.dbg_meta[row * 2] = 0;
+                a.dbg_meta[row * 2 + 1] = 0;
+            }
+            publish(a, row, 0);
+        }
+        return;
+    }
+    const float maxl = unord_f32(o0);
+    // (all lanes call these: the exp table is read across lanes)
+    auto e_of = [&](uint32_t o) { return expf_glibc_tab(__fdiv_rn(__fsub_rn(unord_f32(o), maxl), p.temperature), tab); };
+    // softmax total (:53-60) and kk, the candidates that are numbers (a prefix of the sorted keys)
+    double sum = 0.0;
+    int kk = 0;
+    for (int c = 0; c < k; c += 64) {
+        const uint32_t o = img(c + lane, k);
+        const double e = (double) e_of(o);
+        const int nv = __popcll(ballot(o != 0u));
+        for (int j = 0; j < nv; ++j) sum = __dadd_rn(sum, rdlaned(e, j));
+        kk = c + nv;
+        if (nv < 64) break;
+    }
+    auto p_of = [&](uint32_t o) { return __double2float_rn(__ddiv_rn((double) e_of(o), sum)); };
+    // min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
+    int n = kk;
+    if (p.min_p > 0.0f) {
+        const float thr = __fmul_rn(p_of(o0), p.min_p);
+        for (int c = 0; c < kk; c += 64) {
+            const int i = c + lane;
+            const float pi = p_of(img(i, kk));
+            const uint64_t fail = ballot(i < kk && i >= 1 && !(pi >= thr));
+            if (fail) {
+                n = c + __builtin_ctzll(fail);
+                break;
+            }
+        }
+    }
+    // top-p (:69-79): cum over the candidates until it reaches top_p; the draw total (:80-81) is the same chain
+    // over the kept ones
+    double total = 0.0;
+    if (p.top_p < 1.0f) {
+        int m = n;
+        for (int c = 0; c < n && m == n; c += 64) {
+            const double pi = (double) p_of(img(c + lane, n));
+            const int nv = min(64, n - c);
+            for (int j = 0; j < nv; ++j) {
+                total = __dadd_rn(total, rdlaned(pi, j));
+                if (total >= (double) p.top_p) {
+                    m = c + j + 1;
+                    break;
+                }
+            }
+        }
+        n = max(m, 1);
+    } else {
+        for (int c = 0; c < n; c += 64) {
+            const double pi = (double) p_of(img(c + lane, n));
+            const int nv = min(64, n - c);
+            for (int j = 0; j < nv; ++j) total = __dadd_rn(total, rdlaned(pi, j));
+        }
+    }
+    // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate)
+    double r = __dadd_rn(__dmul_rn(u_row, __dsub_rn(total, 0.0)), 0.0);
+    int idx = n - 1;
+    for (int c = 0; c < n && idx == n - 1; c += 64) {
+        const double pi = (double) p_of(img(c + lane, n));
+        const int nv = min(64, n - c);
+        for (int j = 0; j < nv; ++j) {
+            r = __dsub_rn(r, rdlaned(pi, j));
+            if (r <= 0.0) {
+                idx = c + j;
+                break;
+            }
+        }
+    }
+    const int tok = (int) (~(uint32_t) K[idx] & idm);
+    const uint32_t ol = img(lane, kk);
+    const float pl = p_of(ol);
+    if (a.dbg_keys)
+        a.dbg_keys[row * KCAP + lane] = ol ? ((uint64_t) ol << 32) | (uint64_t) ~(~(uint32_t) K[lane] & idm) : 0ull;
+    if (a.dbg_probs) a.dbg_probs[row * KCAP + lane] = ol ? pl : 0.0f;
+    if (lane == 0) {
+        if (a.dbg_meta) {
+            a.dbg_meta[row * 2] = kk;
+            a.dbg_meta[row * 2 + 1] = n;
+        }
+        publish(a, row, tok);
+    }
+}
+
 // LDS of the history count table: 4 bytes per id for 4-wave workgroups, 2 for 16-wave ones.
 template <bool P, int NW, int EPT>
 constexpr size_t table_bytes() {
@@ -1357,6 +1508,36 @@ hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_
     if (a.p.k < 1 || a.p.k > KCAP) return hipErrorInvalidValue;
     if (greedy) return penalize ? launch_gp<true, true>(a, s) : launch_gp<true, false>(a, s);
     return penalize ? launch_gp<false, true>(a, s) : launch_gp<false, false>(a, s);
+}
+
+int wide_id_bits(int V) {
+    int b = 1;
+    while (b < 31 && (1ll << b) < (long long) V) ++b;
+    return b;
+}
+
+hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipStream_t s) {
+    if (w.k <= KCAP || w.k > a.V) return hipErrorInvalidValue;
+    const int segs = (a.V + WIDE_SEG - 1) / WIDE_SEG;
+    const dim3 grid((unsigned) (a.n_rows * segs));
+    if (penalize)
+        hipLaunchKernelGGL(wide_keys_kernel<true>, grid, dim3(WIDE_WG), WIDE_SEG * sizeof(uint32_t), s, a, w);
+    else
+        hipLaunchKernelGGL(wide_keys_kernel<false>, grid, dim3(WIDE_WG), 0, s, a, w);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    int rb = 0;
+    while ((1 << rb) < a.n_rows) ++rb;
+    const size_t n = (size_t) a.n_rows * a.V;
+    size_t need = 0;
+    e = sort_keys_desc(nullptr, &need, w.keys, w.sorted, n, 32 + w.id_bits + rb, s);  // (a size query)
+    if (e != hipSuccess) return e;
+    if (need > w.sort_tmp_bytes) return hipErrorInvalidValue;
+    size_t bytes = w.sort_tmp_bytes;
+    e = sort_keys_desc(w.sort_tmp, &bytes, w.keys, w.sorted, n, 32 + w.id_bits + rb, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(64), 0, s, a, w);
+    return hipGetLastError();
 }
 
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s) {

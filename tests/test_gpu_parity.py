@@ -45,12 +45,14 @@ def check_row(S, O, row_logits, p, u, counts, label):
 
 
 def assert_same_candidates(O_ids, O_probs, O_kept, gi, gp, gk, gkept, label, k_expected=None):
+    # (above 64 candidates, the handle reports the first 64 of them and the full count)
     n = len(O_ids)
-    if n <= 64:
+    m = min(n, 64)
+    if n < 4096:
         assert gk == n, (label, gk, n)
-        assert list(gi) == list(O_ids), label
-        assert gp.tobytes() == O_probs.tobytes(), (label, np.max(np.abs(gp - O_probs) / np.maximum(O_probs, 1e-30)))
-        assert gkept == O_kept, label
+    assert list(gi) == list(O_ids[:m]), label
+    assert gp.tobytes() == O_probs[:m].tobytes(), (label, np.max(np.abs(gp - O_probs[:m]) / np.maximum(O_probs[:m], 1e-30)))
+    assert gkept == O_kept, label
 
 
 def test_expf_bitexact_vs_host_libm(torch_cuda, K, oracle_lib):
@@ -171,7 +173,7 @@ _rng = np.random.default_rng(2026)
 for V in (1, 3, 64, 100, 1000, 1023, 1025, 4096, 8193, 50000, 248320):
     for _ in range(3 if V < 248320 else 2):
         T = float(_rng.choice([0.0, 0.3, 1.0, 2.0]))
-        k = int(_rng.choice([1, 2, 20, 63, 64]))
+        k = int(_rng.choice([1, 2, 20, 63, 64, 65, 300]))
         pen = int(_rng.integers(0, 3))
         CASES.append((V, T, k, pen, int(_rng.integers(1, 2**31))))
 
@@ -181,9 +183,6 @@ def test_random_rows(torch_cuda, K, oracle_lib, V, T, k, pen, seed):
     torch = torch_cuda
     O = oracle_lib
     rng = np.random.default_rng(seed)
-    kk = k if k < V else V
-    if T > 0 and kk > 64:
-        pytest.skip("k above 64")
     x = (rng.standard_normal(V) * rng.uniform(0.5, 3)).astype(np.float32)
     if V > 10:
         x[rng.choice(V, min(V // 3, 40), replace=False)] = np.float32(rng.choice([2.5, 4.0]))  # exact ties
@@ -195,8 +194,6 @@ def test_random_rows(torch_cuda, K, oracle_lib, V, T, k, pen, seed):
     elif pen == 2:
         pp.update(presence_penalty=-0.8, frequency_penalty=-0.1, repetition_penalty=0.7)
     p = W.Params(**pp)
-    if T > 0 and not (0 < p.top_k < V) and V > 64:
-        p.top_k = k
     hist = rng.integers(0, V, int(rng.integers(0, 600))).astype(np.int32) if pen else np.zeros(0, np.int32)
     S = K.Sampler(p, n_vocab=V)
     for t in hist:

@@ -1,0 +1,168 @@
+"""GPU parity of the wide top-k path (top_k above 64, or no limit: src/sampler.cpp:42-51 with k up to V): every
+logit keyed and sorted on the device, then the reference's tail over the sorted candidates. Token ids, the first
+64 candidates (ids and probabilities), the candidate count and the kept count bit-exact against the oracle, with
+and without penalties, through the batch entry point, single-row sampling and the verify step."""
+import numpy as np
+import pytest
+
+from klein_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    torch.cuda.init()
+    return torch
+
+
+@pytest.fixture(scope="module")
+def K():
+    import klein_amd
+    return klein_amd
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def head_rows(rng, rows, V, scale=1.5):
+    x = (rng.standard_normal((rows, V)) * scale).astype(np.float32)
+    for r in range(rows):
+        heads = rng.choice(V, min(50, V), replace=False)
+        x[r, heads] = (8 + 2 * rng.standard_normal(len(heads))).astype(np.float32)
+        x[r, rng.choice(V, min(12, V), replace=False)] = np.float32(9.5)  # exact ties among the heads
+    return x
+
+
+def zipf_history(rng, V, n):
+    ranks = np.minimum(rng.zipf(1.1, n), V) - 1
+    return rng.permutation(V)[ranks].astype(np.int32)
+
+
+def check_row(S, O, x, p, u, counts, r, label):
+    t, oids, probs, kept = O.sample(x, p, float(u), counts, O.MODE_TOTAL, cap=64)
+    gi, gp, gk, gkept = S.candidates(r)
+    k_ref = p.top_k if 0 < p.top_k < x.shape[0] else x.shape[0]
+    assert gk == k_ref, (label, r, gk, k_ref)
+    assert list(gi) == list(oids), (label, r)
+    assert gp.tobytes() == probs.tobytes(), (label, r)
+    assert gkept == kept, (label, r, gkept, kept)
+    return t
+
+
+PENS = {
+    0: {},
+    1: dict(presence_penalty=0.5, frequency_penalty=0.2, repetition_penalty=1.1),
+    2: dict(presence_penalty=-0.8, frequency_penalty=-0.1, repetition_penalty=0.7),
+}
+
+BATCH_CASES = [
+    # V, rows, temperature, top_k, top_p, min_p, penalties, history length
+    (70001, 3, 1.0, 65, 0.9, 0.0, 1, 3000),
+    (70001, 2, 0.7, 1000, 0.95, 0.05, 2, 2000),
+    (248320, 2, 1.0, 0, 0.95, 0.0, 1, 16384),
+    (248320, 2, 1.3, 200, 1.0, 0.0, 0, 0),
+    (5000, 3, 2.0, 0, 0.999, 0.0, 0, 0),
+    (100, 2, 1.0, 0, 1.0, 0.01, 1, 300),
+]
+
+
+@pytest.mark.parametrize("case", range(len(BATCH_CASES)))
+def test_wide_batch(torch_cuda, K, oracle_lib, case):
+    torch = torch_cuda
+    O = oracle_lib
+    V, rows, T, k, tp, mp, pen, nh = BATCH_CASES[case]
+    rng = np.random.default_rng(900 + case)
+    x = head_rows(rng, rows, V)
+    p = W.Params(temperature=T, top_k=k, top_p=tp, min_p=mp, **PENS[pen])
+    hists = [zipf_history(rng, V, nh) if nh else np.zeros(0, np.int32) for _ in range(rows)]
+    if pen:
+        for r in range(rows):  # push some heads through the penalties
+            hists[r] = np.concatenate([hists[r], np.argsort(-x[r])[:30].astype(np.int32)])
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum([len(h) for h in hists])
+    ids = np.concatenate(hists).astype(np.int32) if off[-1] else np.zeros(1, np.int32)
+    u = rng.random(rows)
+    u[0] = 0.9999999
+    S = K.Sampler(p, n_vocab=V, max_rows=rows)
+    out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    say("wide batch", case, "V", V, "k", k, "rows", rows)
+    if pen:
+        S.sample_batch(dev(torch, x), dev(torch, u), out, dev(torch, off), dev(torch, ids))
+    else:
+        S.sample_batch(dev(torch, x), dev(torch, u), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        counts = W.counts_of(hists[r], V) if pen else None
+        t = check_row(S, O, x[r], p, u[r], counts, r, f"case{case}")
+        assert got[r] == t, (case, r, got[r], t)
+    S.close()
+
+
+def test_wide_ties_and_infinities(torch_cuda, K, oracle_lib):
+    """Every logit equal (candidate order is id order), and rows with -inf logits, under no top-k limit."""
+    torch = torch_cuda
+    O = oracle_lib
+    V = 3000
+    x = np.zeros((3, V), np.float32)
+    x[1, ::3] = -np.inf
+    x[2] = np.where(np.arange(V) % 7 == 0, np.float32(2.0), np.float32(-np.inf))
+    p = W.Params(temperature=1.0, top_k=0, top_p=0.5, min_p=0.0)
+    u = np.array([0.3, 0.9999, 0.5])
+    S = K.Sampler(p, n_vocab=V, max_rows=3)
+    out = torch.full((3,), -1, dtype=torch.int32, device="cuda")
+    say("wide ties")
+    S.sample_batch(dev(torch, x), dev(torch, u), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(3):
+        t = check_row(S, O, x[r], p, u[r], None, r, "ties")
+        assert got[r] == t, (r, got[r], t)
+    S.close()
+
+
+def test_wide_sample_and_verify_with_history(torch_cuda, K, oracle_lib):
+    """The handle's own history (accepted tokens counted on the device) with k above 64: single-row samples,
+    then verify steps with drafts."""
+    O = oracle_lib
+    V = 70001
+    rng = np.random.default_rng(77)
+    p = W.Params(temperature=0.9, top_k=500, top_p=0.9, min_p=0.02, presence_penalty=0.4, frequency_penalty=0.1,
+                 repetition_penalty=1.15, seed=3)
+    S = K.Sampler(p, n_vocab=V, max_rows=4)
+    counts = np.zeros(V, np.int32)
+    for t in rng.integers(0, V, 300):
+        S.accept(int(t))
+        counts[t] += 1
+    for step in range(3):
+        x = head_rows(rng, 1, V)[0]
+        u = float(rng.random())
+        say("wide sample", step)
+        got = S.sample(x, u=u)
+        t = O.sample(x, p, u, counts, O.MODE_TOTAL)[0]
+        assert got == t, (step, got, t)
+        S.accept(got)
+        counts[got] += 1
+    nb = 4
+    for step in range(3):
+        x = head_rows(rng, nb, V)
+        u = rng.random(nb)
+        m = int(rng.integers(0, nb))
+        drafts = rng.integers(0, V, nb - 1).astype(np.int32)
+        c = counts.copy()
+        for i in range(m):
+            drafts[i] = O.sample(x[i], p, u[i], c, O.MODE_TOTAL)[0]
+            c[drafts[i]] += 1
+        say("wide verify", step, "m", m)
+        toks, acc = S.verify(x, drafts, u=u)
+        ot, oa, counts = O.verify(x, drafts, p, u, counts, O.MODE_TOTAL)
+        assert acc == oa and list(toks) == list(ot[:oa + 1]), (step, acc, oa)
+    S.close()
