@@ -1338,105 +1338,136 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
     }
 }
 
-// The tail of src/sampler.cpp:53-88 over a row's sorted keys, one wave per row: candidate i is the row's i-th
-// key (value descending, id ascending), numbers only (NaN keys sort last and are left out). Every sum is the
-// reference's sequential double chain, one addition per candidate in candidate order; each pass walks the
-// candidates in chunks of 64 (lane j holding candidate c + j) and recomputes e_i and p_i as it goes.
-__global__ __launch_bounds__(64) void wide_tail_kernel(RowsArgs a, WideArgs w) {
-    const int row = (int) blockIdx.x, lane = (int) threadIdx.x;
+// The tail of src/sampler.cpp:53-88 over a row's sorted keys (one workgroup per row): candidate i is the row's
+// i-th key (value descending, id ascending), numbers only (NaN keys sort last and are left out). The per-candidate
+// terms (e_i, then p_i) are computed by every thread into the row's part of the key buffer (free after the
+// sort) as doubles; every sum is then the reference's sequential double chain, one addition per candidate in
+// candidate order, run by wave 0 over 64-candidate chunks (lane j holding candidate c + j) with the loads of the
+// next chunks in flight.
+constexpr int TAIL_WG = 1024;
+constexpr int TAIL_AHEAD = 4;  // chunks loaded ahead of the chain
+
+__shared__ int s_wide_n;    // kk, then the min-p length
+__shared__ double s_wide_sum;
+
+// Sequential double chain over terms t[0..n) (wave 0): f(acc, i, term) returns false to stop after term i.
+template <typename F>
+__device__ __forceinline__ double chain(const double* __restrict__ t, int n, double acc, int lane, F f) {
+    double nxt[TAIL_AHEAD];
+#pragma unroll
+    for (int q = 0; q < TAIL_AHEAD; ++q) nxt[q] = (64 * q + lane < n) ? t[64 * q + lane] : 0.0;
+    for (int c = 0; c < n; c += 64 * TAIL_AHEAD) {
+        double cur[TAIL_AHEAD];
+#pragma unroll
+        for (int q = 0; q < TAIL_AHEAD; ++q) {
+            cur[q] = nxt[q];
+            const int i = c + 64 * (TAIL_AHEAD + q) + lane;
+            nxt[q] = i < n ? t[i] : 0.0;
+        }
+#pragma unroll
+        for (int q = 0; q < TAIL_AHEAD; ++q) {
+            const int c0 = c + 64 * q;
+            const int nv = min(64, n - c0);
+            for (int j = 0; j < nv; ++j) {
+                acc = __dadd_rn(acc, rdlaned(cur[q], j));
+                if (!f(acc, c0 + j)) return acc;
+            }
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs w) {
+    const int row = (int) blockIdx.x, tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
     const int ib = w.id_bits, k = w.k;
     const uint64_t vmask = (1ull << (32 + ib)) - 1ull;
     const uint32_t idm = (1u << ib) - 1u;
     const uint64_t* __restrict__ K = w.sorted + (int64_t) row * a.V;
+    double* __restrict__ t = reinterpret_cast<double*>(w.keys + (int64_t) row * a.V);  // per-candidate terms
     const SamplingParams p = a.p;
-    const uint64_t tab = kExp2Tab[lane & 31];
-    const double u_row = a.u[row];
-    auto img = [&](int i, int lim) { return i < lim ? (uint32_t) ((K[i] & vmask) >> ib) : 0u; };  // 0: none
-    const uint32_t o0 = img(0, 1);
+    auto img = [&](int i) { return (uint32_t) ((K[i] & vmask) >> ib); };  // value image, 0: NaN
+    const uint32_t o0 = img(0);
     if (o0 == 0u) {  // no number in the row: the fast path's empty candidate list
-        if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = 0ull;
-        if (lane == 0) {
-            if (a.dbg_meta) {
-                a.dbg_meta[row * 2] = 0;
-                a.dbg_meta[row * 2 + 1] = 0;
+        if (wave == 0) {
+            if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = 0ull;
+            if (lane == 0) {
+                if (a.dbg_meta) {
+                    a.dbg_meta[row * 2] = 0;
+                    a.dbg_meta[row * 2 + 1] = 0;
+                }
+                publish(a, row, 0);
             }
-            publish(a, row, 0);
         }
         return;
     }
     const float maxl = unord_f32(o0);
-    // (all lanes call these: the exp table is read across lanes)
-    auto e_of = [&](uint32_t o) { return expf_glibc_tab(__fdiv_rn(__fsub_rn(unord_f32(o), maxl), p.temperature), tab); };
-    // softmax total (:53-60) and kk, the candidates that are numbers (a prefix of the sorted keys)
-    double sum = 0.0;
-    int kk = 0;
-    for (int c = 0; c < k; c += 64) {
-        const uint32_t o = img(c + lane, k);
-        const double e = (double) e_of(o);
-        const int nv = __popcll(ballot(o != 0u));
-        for (int j = 0; j < nv; ++j) sum = __dadd_rn(sum, rdlaned(e, j));
-        kk = c + nv;
-        if (nv < 64) break;
+    // e_i (:55-58) of every candidate, and kk: the first NaN key ends the candidates
+    if (tid == 0) s_wide_n = k;
+    __syncthreads();
+    for (int i = tid; i < k; i += TAIL_WG) {
+        const uint32_t o = img(i);
+        if (o == 0u) atomicMin(&s_wide_n, i);
+        t[i] = (double) expf_glibc(__fdiv_rn(__fsub_rn(unord_f32(o), maxl), p.temperature));
     }
-    auto p_of = [&](uint32_t o) { return __double2float_rn(__ddiv_rn((double) e_of(o), sum)); };
-    // min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
-    int n = kk;
-    if (p.min_p > 0.0f) {
-        const float thr = __fmul_rn(p_of(o0), p.min_p);
-        for (int c = 0; c < kk; c += 64) {
-            const int i = c + lane;
-            const float pi = p_of(img(i, kk));
-            const uint64_t fail = ballot(i < kk && i >= 1 && !(pi >= thr));
-            if (fail) {
-                n = c + __builtin_ctzll(fail);
-                break;
-            }
-        }
+    __syncthreads();
+    const int kk = s_wide_n;
+    // the softmax total (:58), sequential
+    if (wave == 0) {
+        const double sum = chain(t, kk, 0.0, lane, [](double, int) { return true; });
+        if (lane == 0) s_wide_sum = sum;
     }
+    __syncthreads();
+    const double sum = s_wide_sum;
+    // p_i (:60), and min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
+    const double e0 = (double) expf_glibc(__fdiv_rn(__fsub_rn(maxl, maxl), p.temperature));
+    const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
+    if (tid == 0) s_wide_n = kk;
+    __syncthreads();
+    for (int i = tid; i < kk; i += TAIL_WG) {
+        const float pi = __double2float_rn(__ddiv_rn(t[i], sum));
+        if (p.min_p > 0.0f && i >= 1 && !(pi >= thr)) atomicMin(&s_wide_n, i);
+        t[i] = (double) pi;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    int n = s_wide_n;
     // top-p (:69-79): cum over the candidates until it reaches top_p; the draw total (:80-81) is the same chain
     // over the kept ones
-    double total = 0.0;
+    double total;
     if (p.top_p < 1.0f) {
         int m = n;
-        for (int c = 0; c < n && m == n; c += 64) {
-            const double pi = (double) p_of(img(c + lane, n));
-            const int nv = min(64, n - c);
-            for (int j = 0; j < nv; ++j) {
-                total = __dadd_rn(total, rdlaned(pi, j));
-                if (total >= (double) p.top_p) {
-                    m = c + j + 1;
-                    break;
-                }
+        const double tp = (double) p.top_p;
+        total = chain(t, n, 0.0, lane, [&](double acc, int i) {
+            if (acc >= tp) {
+                m = i + 1;
+                return false;
             }
-        }
+            return true;
+        });
         n = max(m, 1);
     } else {
-        for (int c = 0; c < n; c += 64) {
-            const double pi = (double) p_of(img(c + lane, n));
-            const int nv = min(64, n - c);
-            for (int j = 0; j < nv; ++j) total = __dadd_rn(total, rdlaned(pi, j));
-        }
+        total = chain(t, n, 0.0, lane, [](double, int) { return true; });
     }
-    // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate)
-    double r = __dadd_rn(__dmul_rn(u_row, __dsub_rn(total, 0.0)), 0.0);
+    // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a chain
+    // of additions of -p_i (exactly the subtractions)
+    const double r0 = __dadd_rn(__dmul_rn(a.u[row], __dsub_rn(total, 0.0)), 0.0);
+    const bool act = lane < kk;
+    const float dbg_p = act ? (float) t[lane] : 0.0f;
     int idx = n - 1;
-    for (int c = 0; c < n && idx == n - 1; c += 64) {
-        const double pi = (double) p_of(img(c + lane, n));
-        const int nv = min(64, n - c);
-        for (int j = 0; j < nv; ++j) {
-            r = __dsub_rn(r, rdlaned(pi, j));
-            if (r <= 0.0) {
-                idx = c + j;
-                break;
-            }
-        }
+    for (int c = 0; c < n; c += 64) {  // (p_i negated in place for the chain)
+        if (c + lane < n) t[c + lane] = -t[c + lane];
     }
+    chain(t, n, r0, lane, [&](double r, int i) {
+        if (r <= 0.0) {
+            idx = i;
+            return false;
+        }
+        return true;
+    });
     const int tok = (int) (~(uint32_t) K[idx] & idm);
-    const uint32_t ol = img(lane, kk);
-    const float pl = p_of(ol);
-    if (a.dbg_keys)
-        a.dbg_keys[row * KCAP + lane] = ol ? ((uint64_t) ol << 32) | (uint64_t) ~(~(uint32_t) K[lane] & idm) : 0ull;
-    if (a.dbg_probs) a.dbg_probs[row * KCAP + lane] = ol ? pl : 0.0f;
+    const uint32_t ol = act ? img(lane) : 0u;
+    if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = act ? ((uint64_t) ol << 32) | (uint64_t) ~(~(uint32_t) K[lane] & idm) : 0ull;
+    if (a.dbg_probs) a.dbg_probs[row * KCAP + lane] = dbg_p;
     if (lane == 0) {
         if (a.dbg_meta) {
             a.dbg_meta[row * 2] = kk;
@@ -1536,7 +1567,7 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
     size_t bytes = w.sort_tmp_bytes;
     e = sort_keys_desc(w.sort_tmp, &bytes, w.keys, w.sorted, n, 32 + w.id_bits + rb, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(64), 0, s, a, w);
+    hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(TAIL_WG), 0, s, a, w);
     return hipGetLastError();
 }
 
