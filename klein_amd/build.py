@@ -39,5 +39,19 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+
+def build_dropin_check() -> str:
+    """tests/cpp/dropin_check: a C++ program that uses klein::Sampler (csrc/sampler.h) through the library."""
+    src = os.path.join(ROOT, "tests", "cpp", "dropin_check.cpp")
+    exe = os.path.join(ROOT, "tests", "cpp", "dropin_check")
+    cmd = [os.environ.get("CXX", "g++"), "-std=c++17", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+           src, "-L", LIBDIR, "-lklein_sampler", "-Wl,-rpath,$ORIGIN/../../klein_amd/lib", "-o", exe]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("building tests/cpp/dropin_check failed")
+    return exe
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
