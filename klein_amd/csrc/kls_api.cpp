@@ -50,7 +50,7 @@ struct kls_sampler {
     int k = 0;
     int V = 0, max_rows = 0, device = 0;
     int bucket_shift = MIN_BUCKET_SHIFT, n_buckets = 0;
-    int seg_len_override = 0, target_wg = 300, wide_target_wg = 320, share_min_wg = 1024, xcd_map = 1;
+    int seg_len_override = 0, target_wg = 128, wide_target_wg = 320, share_min_wg = 1024, xcd_map = 1;
     hipStream_t stream = nullptr;
 
     // token history: host copy (as the reference's counts_) + what has reached the device
@@ -109,7 +109,8 @@ bool is_device_ptr(const void* p) {
 }
 
 // Segment length. Short segments (256 threads x {4, 8, 16, 32} logits): the smallest length whose grid (rows x
-// segments) stays within target_wg workgroups, so small batches spread over every CU. When even 8192 ids leave
+// segments) stays within target_wg workgroups (128: half the CUs; every segment of a row then takes the row's
+// ticket, and more segments wait longer on it than their shorter reads save). When even 8192 ids leave
 // too many workgroups, 1024-thread workgroups over 16384..65536 ids (one per CU), the smallest length within
 // wide_target_wg: every logit and the row's history are then read once per segment with the chip full.
 void segments_for(const kls_sampler* h, int rows, int* seg_len, int* segs) {

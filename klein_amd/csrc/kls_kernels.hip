@@ -7,8 +7,8 @@
 //   * penalties (sampler.cpp:18-29) are applied in-register by the one lane holding each id, from a count table
 //     of the segment's history ids staged in LDS; nothing is written to the logits or any global buffer;
 //   * greedy (sampler.cpp:31-39) keeps a per-lane (max, first id) and reduces across lanes and segments;
-//   * top-k (sampler.cpp:42-51): every lane contributes its two largest logits; the k-th largest of those
-//     (2 x NW*64 distinct logits) is a lower bound of the segment's k-th largest value, and with the best bound
+//   * top-k (sampler.cpp:42-51): every lane contributes its largest logit; the k-th largest of those
+//     (NW*64 distinct logits) is a lower bound of the segment's k-th largest value, and with the best bound
 //     other workgroups of the row have published, one float compare per logit rejects nearly everything. The
 //     few survivors are ordered by a 64-bit key (value descending, id ascending) with wave64 bitonic networks
 //     built from DPP and permlane swaps;
@@ -838,14 +838,17 @@ __device__ int sample_tail(uint64_t lst, int kk, const SamplingParams p, double 
 }
 
 // Publishes row `row`'s token: device output, and for the host one 64-bit word (sequence number, token).
-__device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok) {
+// `seq` is the call's sequence number (call_seq, read ahead: the call block is host memory).
+__device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok, uint32_t seq) {
     a.out_tokens[row] = tok;
     a.row_ticket[row] = 0u;
     if (a.share_bounds) a.row_thr[row] = 0ull;
     if (a.host_res && row < VERIFY_MAX_ROWS)
-        __hip_atomic_store(&a.host_res->row_word[row], ((uint64_t) a.call->seq << 32) | (uint32_t) tok,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(&a.host_res->row_word[row], ((uint64_t) seq << 32) | (uint32_t) tok, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
 }
+
+__device__ __forceinline__ uint32_t call_seq(const RowsArgs& a) { return a.host_res ? a.call->seq : 0u; }
 
 // Loads this thread's logits of groups I0 <= i < I1: ids lb + 4*(i*WG + tid) + e.
 //  * FULL: every group is a whole aligned float4 inside the row, read through the buffer resource `seg` (base =
@@ -913,6 +916,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     const bool vec = ((a.row_stride & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0);
     const int k = a.p.k;
     uint64_t* seg_out = a.seg_cand + ((int64_t) row * a.segs + seg) * KCAP;
+    // what the row's last workgroup will need from host memory (the pinned call block, for graph-replayed
+    // steps), read now so that its latency is hidden behind the segment's
+    const uint32_t seq = call_seq(a);
+    const double u_row = GREEDY ? 0.0 : a.u[row];
     // a bound other workgroups of the row published (large grids only): read before the logits arrive
     const uint64_t t_row =
         a.share_bounds ? __hip_atomic_load(&a.row_thr[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
@@ -1072,9 +1079,8 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         }
         uint32_t gl;
         if constexpr (NW == 4) {
-            const uint32_t l1 = sort32<true>(ord_f32(m1), lane);
-            const uint32_t l2 = sort32<false>(pen_lazy ? 0u : ord_f32(m2), lane);  // (lazy: raw m2 has no id)
-            s_mx<NW>[wave][lane] = bitonic_stage32<64, true>(max(l1, l2), lane);
+            // 4 waves: each sorts its lane maxima, every wave merges the four lists
+            s_mx<NW>[wave][lane] = sort32<true>(ord_f32(m1), lane);
             __syncthreads();
             gl = s_mx<NW>[0][lane];
 #pragma unroll
@@ -1171,14 +1177,13 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                     a.dbg_meta[row * 2] = 0;
                     a.dbg_meta[row * 2 + 1] = 0;
                 }
-                publish(a, row, m ? key_id(m) : 0);  // all -inf / NaN: the reference returns id 0
+                publish(a, row, m ? key_id(m) : 0, seq);  // all -inf / NaN: the reference returns id 0
             }
             return;
         }
         // The lists (each sorted, the first k entries valid) are merged as a tree: pairs, then pairs of pairs.
         // Every lane loads from every list slot (clamped to the row's lists; entries past k are stale and zeroed),
         // so the loads are issued together, with the row's uniform. Odd lists are read reversed (ascending).
-        const double u_row = a.u[row];
         const uint64_t exp_tab = kExp2Tab[lane & 31];
         uint64_t lk[8];
 #pragma unroll
@@ -1203,7 +1208,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
         const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
                                     a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
-        if (lane == 0) publish(a, row, tok);
+        if (lane == 0) publish(a, row, tok, seq);
         return;
     }
     __syncthreads();
@@ -1228,7 +1233,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             a.dbg_meta[row * 2] = 0;
             a.dbg_meta[row * 2 + 1] = 0;
         }
-        publish(a, row, m ? key_id(m) : 0);  // all -inf / NaN: the reference returns id 0
+        publish(a, row, m ? key_id(m) : 0, seq);  // all -inf / NaN: the reference returns id 0
         return;
     }
 
@@ -1243,7 +1248,6 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     const bool one = nH <= 64;
     const int h = one ? (wave == 0 ? lane : WG) : lane * NW + wave;
     // (loads clamped to the row's lists and issued together; what is out of range is zeroed after)
-    const double u_row = a.u[row];
     const uint64_t exp_tab = kExp2Tab[lane & 31];
     const int hc = min(h, nH - 1);
     uint64_t hv = load_dev(&cand[(int64_t) (hc / J) * KCAP + hc % J]);
@@ -1287,7 +1291,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
     const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
                                 a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
-    if (lane == 0) publish(a, row, tok);
+    if (lane == 0) publish(a, row, tok, seq);
 }
 
 __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
@@ -1385,6 +1389,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
     const uint64_t* __restrict__ K = w.sorted + (int64_t) row * a.V;
     double* __restrict__ t = reinterpret_cast<double*>(w.keys + (int64_t) row * a.V);  // per-candidate terms
     const SamplingParams p = a.p;
+    const uint32_t seq = call_seq(a);
     auto img = [&](int i) { return (uint32_t) ((K[i] & vmask) >> ib); };  // value image, 0: NaN
     const uint32_t o0 = img(0);
     if (o0 == 0u) {  // no number in the row: the fast path's empty candidate list
@@ -1395,7 +1400,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
                     a.dbg_meta[row * 2] = 0;
                     a.dbg_meta[row * 2 + 1] = 0;
                 }
-                publish(a, row, 0);
+                publish(a, row, 0, seq);
             }
         }
         return;
@@ -1473,7 +1478,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
             a.dbg_meta[row * 2] = kk;
             a.dbg_meta[row * 2 + 1] = n;
         }
-        publish(a, row, tok);
+        publish(a, row, tok, seq);
     }
 }
 
