@@ -43,6 +43,11 @@ template <int NW> __shared__ uint32_t s_mx[NW][64];    // per-wave sorted lane m
 template <int NW> __shared__ uint32_t s_mx4[4][64];    // their merges in groups of four waves
 __shared__ int s_last;
 __shared__ int s_counted;  // waves done counting the history (lazy top-k rows)
+// 16-wave top-k segments: arrivals at the early bound (per group of four waves, then group merges), the bound
+// and its ready flag
+__shared__ int s_arr[4];
+__shared__ uint32_t s_qe;
+__shared__ int s_qready;
 
 
 // ---------------------------------------------------------------------------------------------------------
@@ -931,7 +936,11 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // never held at once.
     const __amdgpu_buffer_rsrc_t seg_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(L + lb), (short) 0, SEG * 4, kRawBufferFlags);
-    constexpr int Q1 = PENALIZE ? (NV >= 16 ? 4 : NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : NV, Q3 = PENALIZE ? NV - NV / 4 : NV;
+    // 16-wave top-k segments take their bound from waves 0..11 (the early bound, below); its LDS counters are
+    // cleared before the barrier that follows the first batch (without penalties: one float4 per thread)
+    constexpr bool EARLY = !GREEDY && NW == 16;
+    constexpr int Q1 = PENALIZE ? (NV >= 16 ? 4 : NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : EARLY ? 1 : NV;
+    constexpr int Q3 = PENALIZE ? NV - NV / 4 : Q1;
     float v[EPT];
     RawHistory rh;
     bool wide = false;
@@ -948,7 +957,13 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     if (PENALIZE) {
         // cleared whatever the table's width turns out to be (wide tables are cleared again per half)
         cnt_zero<WG>(C16 ? (hi - lb + 1) / 2 : hi - lb);
-        if (tid == 0) s_counted = 0;  // (ordered before every increment by the barrier below)
+        if (tid == 0) {
+            s_counted = 0;  // (ordered before every increment by the barrier below)
+            if (EARLY) {
+                s_arr[0] = s_arr[1] = s_arr[2] = s_arr[3] = 0;
+                s_qready = 0;
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
         int4 hq[HR];
 #pragma unroll
@@ -981,6 +996,12 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                 __builtin_amdgcn_sched_barrier(0);  // (the last batch stays after the count)
             }
         }
+    } else if (EARLY) {
+        if (tid == 0) {
+            s_arr[0] = s_arr[1] = s_arr[2] = s_arr[3] = 0;
+            s_qready = 0;
+        }
+        __syncthreads();  // counters cleared
     }
     load_groups<FULL, WG, EPT, Q3, NV>(v, vec, seg_rsrc, L, lb, hi);
     // with penalties (16-bit or narrow tables) the counts are applied group by group as the logits are first
@@ -1086,26 +1107,42 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
 #pragma unroll
             for (int o = 1; o < NW; ++o) gl = merge32(gl, s_mx<NW>[o][63 - lane], lane);
         } else {
-            // 16 waves: the lane maxima only (one sort per wave); groups of four lists are merged by waves 0..3,
-            // their four results by wave 0
-            s_mx<NW>[wave][lane] = sort32<true>(ord_f32(m1), lane);
-            __syncthreads();
-            if (wave < 4) {
-                gl = s_mx<NW>[4 * wave][lane];
+            // 16 waves: the early bound, from the lane maxima of waves 0..11 alone (768 distinct logits of the
+            // segment, so still reached by k of them). Those waves receive their logits first (loads issue wave by
+            // wave), so the bound is usually ready when waves 12..15 finish their scan, and they filter at once.
+            // Each early wave sorts its lane maxima; the last of each group of four to arrive merges the group's
+            // lists, the last group to finish merges the three groups' and publishes the k-th value. No wave waits
+            // before it has contributed, so every wait below ends.
+            if (wave < 12) {
+                const int g = wave >> 2;
+                s_mx<NW>[wave][lane] = sort32<true>(ord_f32(m1), lane);
+                int n = 0;
+                if (lane == 0) n = __hip_atomic_fetch_add(&s_arr[g], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (rdlanei(n, 0) == 3) {
+                    gl = s_mx<NW>[4 * g][lane];
 #pragma unroll
-                for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx<NW>[4 * wave + o][63 - lane], lane);
-                s_mx4<NW>[wave][lane] = gl;
-            }
-            __syncthreads();
-            if (wave == 0) {
-                gl = s_mx4<NW>[0][lane];
+                    for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx<NW>[4 * g + o][63 - lane], lane);
+                    s_mx4<NW>[g][lane] = gl;
+                    n = 0;
+                    if (lane == 0) n = __hip_atomic_fetch_add(&s_arr[3], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (rdlanei(n, 0) == 2) {
 #pragma unroll
-                for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx4<NW>[o][63 - lane], lane);
-                const uint32_t qw = (uint32_t) rdlanei((int) gl, k - 1);  // all lanes active
-                if (lane == 0) s_q<NW>[0] = qw;
+                        for (int o = 0; o < 3; ++o)
+                            if (o != g) gl = merge32(gl, s_mx4<NW>[o][63 - lane], lane);
+                        const uint32_t qw = (uint32_t) rdlanei((int) gl, k - 1);  // all lanes active
+                        if (lane == 0) {
+                            s_qe = qw;
+                            __hip_atomic_store(&s_qready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        }
+                    }
+                }
             }
-            __syncthreads();
-            gl = s_q<NW>[0];
+            // (the bound on the wait is a guard only)
+            for (int spin = 0; spin < (1 << 20); ++spin) {
+                if (__hip_atomic_load(&s_qready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            gl = s_qe;
         }
         const uint32_t q = NW == 4 ? (uint32_t) rdlanei((int) gl, k - 1) : gl;  // all lanes active
         const float t_f = fmaxf(floor32(q), floor64(t_row));
