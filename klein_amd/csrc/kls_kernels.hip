@@ -984,7 +984,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // (the barrier comes before the rest of the segment: every wave reaches it having issued few loads; a
         // wave whose loads wait for issue slots would hold the others here)
         __syncthreads();  // table zeroed
-        load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
+        // Lazy 16-wave rows: waves 8..15, whose loads wait behind the first half's anyway, count before issuing
+        // the middle batch, so that the table is complete (and the early bound can form) sooner.
+        const bool count_first = late && NW == 16 && wave >= 8;
+        if (!count_first) load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
         if (!wide) {
             count_history<WG, C16, true>(a, row, lb, hi, hq, rh);
             // (before the last batch, for the same reason; late counts are first read after the scan, once every
@@ -996,6 +999,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                 __builtin_amdgcn_sched_barrier(0);  // (the last batch stays after the count)
             }
         }
+        if (count_first) load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
     } else if (EARLY) {
         if (tid == 0) {
             s_arr[0] = s_arr[1] = s_arr[2] = s_arr[3] = 0;
