@@ -96,6 +96,14 @@ int kls_verify_wait(kls_handle h, int32_t* out_tokens, int32_t* out_accepted);
 int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_hist_off,
                      const int32_t* d_hist_ids, const double* d_u, int32_t* d_out_tokens, kls_stream stream);
 
+/* Replaces Engine::mtp_draft_token (src/engine.cpp:413-415): for each of n_rows rows of n_vocab f32 logits on
+ * the device (row r at d_logits + r*row_stride), the index std::max_element returns: the first largest element
+ * under '<', so a NaN never replaces the running maximum and a NaN first element is the result. Indices are
+ * written to d_out[r]. Asynchronous on `stream`; the handle lends its scratch (n_rows <= max_rows, n_vocab equal
+ * to the handle's) and its own history and parameters are not used. */
+int kls_argmax(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, int32_t* d_out,
+               kls_stream stream);
+
 /* The sorted top-k candidates of `row` from the last completed call (kls_sample: row 0): ids, softmax
  * probabilities before min-p/top-p truncation (up to `cap`), k, and how many survived min-p/top-p.
  * Synchronizes the handle's stream. For tests and tooling; not needed on the sampling path. */

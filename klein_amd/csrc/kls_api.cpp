@@ -530,6 +530,23 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
     return KLS_OK;
 }
 
+int kls_argmax(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, int32_t* d_out,
+               kls_stream stream) {
+    if (int st = check_handle(h)) return st;
+    if (!d_logits || !d_out) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (n_rows < 1) return fail(KLS_ERR_INVALID_ARG, "n_rows must be positive");
+    if (n_rows > h->max_rows) return fail(KLS_ERR_RANGE, "n_rows above the handle's capacity");
+    if (row_stride < h->V) return fail(KLS_ERR_INVALID_ARG, "row_stride below n_vocab");
+    (void) hipSetDevice(h->device);
+    hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    RowsArgs a = base_args(h, d_logits, n_rows, row_stride);
+    a.out_tokens = d_out;
+    a.first_nan = 1;
+    // (the greedy kernel: first maximum under '>' from -inf, plus the NaN-first case; no penalties)
+    KLS_HIP(launch_rows(a, true, false, s));
+    return KLS_OK;
+}
+
 int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int cap, int32_t* n_k, int32_t* n_kept) {
     if (int st = check_handle(h)) return st;
     if (row < 0 || row >= h->max_rows) return fail(KLS_ERR_RANGE, "row outside the handle's capacity");

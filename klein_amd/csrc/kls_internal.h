@@ -86,6 +86,7 @@ struct RowsArgs {
     uint32_t* row_ticket;   // [n_rows]
     uint64_t* row_thr;      // [n_rows]
     int32_t share_bounds;   // publish / read per-row lower bounds across workgroups (large grids)
+    int32_t first_nan;      // greedy rows as std::max_element: a NaN first logit is the result
 
     // outputs
     int32_t* out_tokens;    // [n_rows] device

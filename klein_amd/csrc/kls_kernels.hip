@@ -925,6 +925,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // steps), read now so that its latency is hidden behind the segment's
     const uint32_t seq = call_seq(a);
     const double u_row = GREEDY ? 0.0 : a.u[row];
+    // greedy rows as std::max_element (engine.cpp:414): the running maximum starts at the first logit and only
+    // '<' replaces it, so a NaN there is the result; otherwise the result is sampler.cpp's greedy id
+    const float l0 = (GREEDY && a.first_nan) ? L[0] : 0.0f;
+    const bool nan_first = l0 != l0;
     // a bound other workgroups of the row published (large grids only): read before the logits arrive
     const uint64_t t_row =
         a.share_bounds ? __hip_atomic_load(&a.row_thr[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
@@ -1218,7 +1222,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                     a.dbg_meta[row * 2] = 0;
                     a.dbg_meta[row * 2 + 1] = 0;
                 }
-                publish(a, row, m ? key_id(m) : 0, seq);  // all -inf / NaN: the reference returns id 0
+                publish(a, row, nan_first ? 0 : m ? key_id(m) : 0, seq);  // all -inf / NaN: id 0
             }
             return;
         }
@@ -1274,7 +1278,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             a.dbg_meta[row * 2] = 0;
             a.dbg_meta[row * 2 + 1] = 0;
         }
-        publish(a, row, m ? key_id(m) : 0, seq);  // all -inf / NaN: the reference returns id 0
+        publish(a, row, nan_first ? 0 : m ? key_id(m) : 0, seq);  // all -inf / NaN: id 0
         return;
     }
 

@@ -143,6 +143,15 @@ class Sampler:
             None if hist_ids is None else _ptr(hist_ids), None if u is None else _ptr(u), _ptr(out_tokens),
             _stream_ptr(stream)), "kls_sample_batch")
 
+    def argmax(self, logits, out, stream=None):
+        """Engine::mtp_draft_token (src/engine.cpp:413-415) per row of the device tensor logits [rows, V] f32:
+        std::max_element's index into out [rows] i32. Asynchronous on `stream`."""
+        rows, n = int(logits.shape[0]), int(logits.shape[1])
+        self._ensure(n)
+        stride = int(logits.stride(0)) if hasattr(logits, "stride") else n
+        _lib.check(_lib.lib().kls_argmax(self._h, _ptr(logits), rows, stride, _ptr(out), _stream_ptr(stream)),
+                   "kls_argmax")
+
     def candidates(self, row: int = 0, cap: int = 64):
         """(ids, probs, k, kept) of the last call's row: the sorted top-k and softmax probabilities."""
         ids = np.zeros(cap, dtype=np.int32)

@@ -75,6 +75,8 @@ def lib():
         L.orc_expf_compare.argtypes = [C.c_uint32, C.POINTER(C.c_float), C.c_longlong, C.c_int,
                                        C.POINTER(C.c_uint32)]
         L.orc_time_rows.restype = C.c_double
+        L.orc_argmax.argtypes = [C.POINTER(C.c_float), C.c_int]
+        L.orc_argmax.restype = C.c_int32
         L.orc_time_rows.argtypes = [C.POINTER(C.c_float), C.c_int, C.c_int, C.POINTER(OrcParams),
                                     C.POINTER(C.c_int32), C.c_int, C.POINTER(C.c_int32)]
         _lib = L
@@ -152,6 +154,12 @@ def verify(logits: np.ndarray, drafts: np.ndarray, p, u: np.ndarray, counts: np.
     acc = lib().orc_verify(_fp(lg), V, nb, _ip(dr) if dr.size else None, C.byref(ps),
                            None if cnt is None else _ip(cnt), _dp(uu), mode, _ip(toks))
     return toks, int(acc), cnt
+
+
+def argmax(row: np.ndarray) -> int:
+    """Engine::mtp_draft_token (src/engine.cpp:413-415): std::max_element's index over one row."""
+    r = np.ascontiguousarray(row, dtype=np.float32)
+    return int(lib().orc_argmax(_fp(r), int(r.shape[0])))
 
 
 def uniforms(seed: int, n: int, skip: int = 0) -> np.ndarray:

@@ -18,6 +18,9 @@
 //   orc_uniforms         : C++ standard KAT (10000th output of mt19937_64 = 9981545732273789042) and the
 //                          reference's own draws (oracle/_ref with the same seed).
 //   orc_expf_glibc       : exhaustive comparison against the host libm expf over every float in [-110, 89].
+//   orc_argmax           : the library call itself (std::max_element, as engine.cpp:414); checked against the
+//                          textbook loop on small rows and the closed form (first index of the largest value
+//                          among numbers; a NaN first element wins) on planted ties, NaNs and infinities.
 #include <algorithm>
 #include <atomic>
 #include <chrono>
@@ -323,6 +326,9 @@ long long orc_expf_compare(uint32_t lo, const float* gpu, long long n, int nthre
     if (first_bad) *first_bad = (uint32_t) (f == UINT64_MAX ? 0 : f);
     return total;
 }
+
+// Engine::mtp_draft_token (src/engine.cpp:413-415): the index std::max_element returns over one row.
+int32_t orc_argmax(const float* logits, int n) { return (int32_t) (std::max_element(logits, logits + n) - logits); }
 
 // Times `reps` Sampler::sample calls on `n_rows` rows of logits (row r at logits + r*n_vocab), cycling through the
 // rows, on one host thread; returns total seconds. Used for the CPU baseline when the reference build is absent.

@@ -130,6 +130,55 @@ def test_greedy_closed_form(oracle_lib):
     assert oracle_lib.sample(x, W.Params(temperature=0.0), 0.0)[0] == 0
 
 
+def _max_element_loop(x):
+    """The textbook std::max_element: the running maximum starts at element 0 and only '<' replaces it."""
+    best = 0
+    for i in range(1, len(x)):
+        if x[best] < x[i]:
+            best = i
+    return best
+
+
+def _max_element_closed(x):
+    """Closed form: a NaN first element is the result; otherwise the first index of the largest number (NaNs
+    never compare larger), and 0 when no element exceeds the first."""
+    if np.isnan(x[0]):
+        return 0
+    num = np.where(np.isnan(x), -np.inf, x)
+    m = num.max()
+    return 0 if m <= x[0] else int(np.argmax(num == m))
+
+
+def test_argmax_matches_textbook_loop_and_closed_form(oracle_lib):
+    """Engine::mtp_draft_token (engine.cpp:413-415) = std::max_element: pinned by the loop definition on small
+    rows and by the closed form on long ones, with planted ties, NaNs and infinities."""
+    rng = np.random.default_rng(11)
+    specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0], dtype=np.float32)
+    for trial in range(400):
+        V = int(rng.integers(1, 40))
+        x = rng.integers(-3, 3, V).astype(np.float32)
+        k = int(rng.integers(0, 4))
+        if k:
+            x[rng.integers(0, V, k)] = specials[rng.integers(0, len(specials), k)]
+        got = oracle_lib.argmax(x)
+        assert got == _max_element_loop(x) == _max_element_closed(x), (trial, x)
+    for trial in range(20):
+        V = int(rng.integers(1000, 300000))
+        x = rng.standard_normal(V).astype(np.float32)
+        x[rng.integers(0, V, 5)] = x.max()  # ties with the maximum
+        if trial % 4 == 1:
+            x[rng.integers(0, V, 50)] = np.nan
+        if trial % 4 == 2:
+            x[0] = np.nan
+        if trial % 4 == 3:
+            x[:] = -np.inf
+        assert oracle_lib.argmax(x) == _max_element_closed(x), trial
+    # (a dropped NaN-first rule or a '<=' comparison each fail one of these)
+    assert oracle_lib.argmax(np.array([np.nan, 1.0, 2.0], np.float32)) == 0
+    assert oracle_lib.argmax(np.array([1.0, 2.0, 2.0], np.float32)) == 1
+    assert oracle_lib.argmax(np.array([-np.inf, np.nan, -np.inf], np.float32)) == 0
+
+
 def test_penalty_closed_form_brute_force(oracle_lib):
     """Tiny vocabulary: greedy over the penalized logits written out with explicit float32 roundings."""
     rng = np.random.default_rng(11)
