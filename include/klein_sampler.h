@@ -104,6 +104,21 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
 int kls_argmax(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, int32_t* d_out,
                kls_stream stream);
 
+/* Replaces the per-token scoring of klein's perplexity / KL-divergence loop (src/main.cpp:308-327) for n_rows
+ * rows of n_vocab f32 logits on the device (row r at d_logits + r*row_stride, target token d_targets[r]):
+ *   d_lse[r] = mx + log(sum_v exp(l[v] - mx)), mx the first largest logit;  d_nll[r] = d_lse[r] - l[target];
+ *   d_top[r] = the index of the first largest logit (std::max_element's rule, as the loop's own scan);
+ * and, with a row of f32 base log-probabilities (d_base, row r at d_base + r*base_stride; NULL for none):
+ *   d_kl[r] = sum over b[v] > -16 of exp(b[v]) * (b[v] - (l[v] - lse));  d_nll_base[r] = -b[target];
+ *   d_base_top[r] = the index of the first largest b.
+ * Every output pointer may be NULL (not written). Sums are in double but in another order than the reference's
+ * sequential loop: values agree to rounding (~1e-15 relative for lse), indices exactly. A NaN logit or an
+ * infinite maximum gives a NaN lse, as in the reference; a target outside [0, n_vocab) gives a NaN nll.
+ * Asynchronous on `stream`; the handle lends its scratch (n_rows <= max_rows, n_vocab equal to the handle's). */
+int kls_ppl_scores(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_targets,
+                   const float* d_base, int64_t base_stride, double* d_lse, double* d_nll, int32_t* d_top,
+                   double* d_kl, double* d_nll_base, int32_t* d_base_top, kls_stream stream);
+
 /* The sorted top-k candidates of `row` from the last completed call (kls_sample: row 0): ids, softmax
  * probabilities before min-p/top-p truncation (up to `cap`), k, and how many survived min-p/top-p.
  * Synchronizes the handle's stream. For tests and tooling; not needed on the sampling path. */

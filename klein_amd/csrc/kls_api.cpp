@@ -547,6 +547,41 @@ int kls_argmax(kls_handle h, const float* d_logits, int n_rows, int64_t row_stri
     return KLS_OK;
 }
 
+int kls_ppl_scores(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_targets,
+                   const float* d_base, int64_t base_stride, double* d_lse, double* d_nll, int32_t* d_top,
+                   double* d_kl, double* d_nll_base, int32_t* d_base_top, kls_stream stream) {
+    if (int st = check_handle(h)) return st;
+    if (!d_logits) return fail(KLS_ERR_INVALID_ARG, "null logits");
+    if (d_nll && !d_targets) return fail(KLS_ERR_INVALID_ARG, "nll needs targets");
+    if ((d_kl || d_nll_base || d_base_top) && !d_base) return fail(KLS_ERR_INVALID_ARG, "KL outputs need a base row");
+    if (d_nll_base && !d_targets) return fail(KLS_ERR_INVALID_ARG, "base nll needs targets");
+    if (n_rows < 1) return fail(KLS_ERR_INVALID_ARG, "n_rows must be positive");
+    if (n_rows > h->max_rows) return fail(KLS_ERR_RANGE, "n_rows above the handle's capacity");
+    if (row_stride < h->V || (d_base && base_stride < h->V)) return fail(KLS_ERR_INVALID_ARG, "row stride below n_vocab");
+    (void) hipSetDevice(h->device);
+    hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    PplArgs a{};
+    a.logits = d_logits;
+    a.row_stride = row_stride;
+    a.base = d_base;
+    a.base_stride = base_stride;
+    a.targets = d_targets;
+    a.V = h->V;
+    a.n_rows = n_rows;
+    a.segs = ppl_segments(h->V, n_rows, &a.seg_len);
+    if (a.segs > h->max_segs) return fail(KLS_ERR_UNSUPPORTED, "ppl segments exceed the scratch");
+    a.scratch = h->d_seg_cand;
+    a.ticket = h->d_row_ticket;
+    a.out_lse = d_lse;
+    a.out_nll = d_nll;
+    a.out_top = d_top;
+    a.out_kl = d_kl;
+    a.out_nll_base = d_nll_base;
+    a.out_base_top = d_base_top;
+    KLS_HIP(launch_ppl(a, s));
+    return KLS_OK;
+}
+
 int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int cap, int32_t* n_k, int32_t* n_kept) {
     if (int st = check_handle(h)) return st;
     if (row < 0 || row >= h->max_rows) return fail(KLS_ERR_RANGE, "row outside the handle's capacity");

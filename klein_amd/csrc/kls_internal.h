@@ -112,6 +112,31 @@ struct WideArgs {
     int32_t id_bits;      // ids are below 1 << id_bits
 };
 
+// Per-token perplexity / KL-divergence scores (src/main.cpp:308-327; kls_ppl.hip). Row r of logits at
+// logits + r*row_stride, of base log-probabilities (optional) at base + r*base_stride; outputs per row, each
+// optional. Scratch: per (row, segment) a KCAP-word record; per row a ticket counter (left zero).
+struct PplArgs {
+    const float* logits;
+    int64_t row_stride;
+    const float* base;
+    int64_t base_stride;
+    const int32_t* targets;
+    int32_t V;
+    int32_t n_rows;
+    int32_t segs;
+    int32_t seg_len;
+    uint64_t* scratch;
+    uint32_t* ticket;
+    double* out_lse;
+    double* out_nll;
+    int32_t* out_top;
+    double* out_kl;
+    double* out_nll_base;
+    int32_t* out_base_top;
+};
+int ppl_segments(int V, int rows, int* seg_len);  // segments per row (and their length) of a launch
+hipError_t launch_ppl(const PplArgs& a, hipStream_t s);
+
 // Launchers (kls_kernels.hip). Return hipSuccess or the launch error.
 hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_t s);
 int rows_grid(const RowsArgs& a);  // workgroups launch_rows starts

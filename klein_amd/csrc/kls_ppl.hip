@@ -1,0 +1,238 @@
+// Per-token scores of klein's perplexity / KL-divergence loop (src/main.cpp:308-327) on gfx950.
+//
+// For each row of logits l (one token position) and its target t the reference computes, in double:
+//   mx   = l[0], raised by every later l[v] > mx (the first largest; imax its index)
+//   lse  = mx + log(sum_v exp((double) l[v] - mx))                     nll = lse - l[t]
+// and, against a row of base log-probabilities b:
+//   kl   = sum_{v: b[v] > -16} exp((double) b[v]) * (b[v] - (l[v] - lse))
+//   ibase = the first largest b (same rule), nll_base = -b[t].
+// The kernel reads every logit (and base entry) once: a workgroup of 256 threads per (row, segment) keeps a
+// running maximum with a rescaled double sum (the sum relative to the maximum so far), the first-maximum keys,
+// and the KL sums split as kl = A + lse * B with A = sum e^b (b - l) and B = sum e^b (both free of lse), so one
+// pass suffices; the row's last workgroup (ticket) combines the segments. The sums run in a different order
+// than the reference's sequential loop, so results agree to rounding (about 1e-15 relative for lse), not bit for
+// bit. NaN and infinities follow the reference: any NaN logit, or an infinite maximum, makes lse NaN (a term
+// exp(NaN) or exp(inf - inf) enters its sum); -inf logits add exp(-inf) = 0.
+#include "kls_internal.h"
+
+namespace kls {
+namespace {
+
+constexpr int PPL_WG = 256;
+constexpr int PPL_NW = PPL_WG / 64;
+
+// value descending, id ascending; NaN maps to 0 (no candidate), -0 is folded onto +0 (they compare equal)
+__device__ __forceinline__ uint64_t num_key(float v, int id) {
+    if (v != v) return 0ull;
+    uint32_t u = __float_as_uint(v);
+    if (v == 0.0f) u = 0u;
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t) o << 32) | (uint64_t) (~(uint32_t) id);
+}
+
+__device__ __forceinline__ int key_index(uint64_t k) { return (int) ~(uint32_t) k; }
+
+__device__ __forceinline__ float key_value(uint64_t k) {
+    const uint32_t o = (uint32_t) (k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+// A running maximum m of the finite logits seen and s = sum over them of exp(x - m).
+struct RunSum {
+    float m = -INFINITY;
+    double s = 0.0;
+    __device__ __forceinline__ void add(float x) {
+        if (!(x - x == 0.0f)) return;  // NaN and infinities are accounted for by the flags
+        if (x > m) {
+            s = s * exp((double) m - (double) x);  // (0 while m is -inf)
+            m = x;
+        }
+        s += exp((double) x - (double) m);
+    }
+    __device__ __forceinline__ void merge(float m2, double s2) {
+        const float mm = fmaxf(m, m2);
+        if (mm == -INFINITY) return;
+        s = (m == -INFINITY ? 0.0 : s * exp((double) m - (double) mm)) +
+            (m2 == -INFINITY ? 0.0 : s2 * exp((double) m2 - (double) mm));
+        m = mm;
+    }
+};
+
+template <typename T>
+__device__ __forceinline__ T shfl_x(T v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+__device__ __forceinline__ uint64_t shfl_x64(uint64_t v, int mask) {
+    const uint32_t lo = (uint32_t) __shfl_xor((int) (uint32_t) v, mask, 64);
+    const uint32_t hi = (uint32_t) __shfl_xor((int) (uint32_t) (v >> 32), mask, 64);
+    return ((uint64_t) hi << 32) | lo;
+}
+
+struct Partial {
+    uint64_t key = 0ull, bkey = 0ull;
+    uint32_t nan = 0u;
+    RunSum r;
+    double a = 0.0, b = 0.0;
+    __device__ __forceinline__ void merge(const Partial& o) {
+        key = key > o.key ? key : o.key;
+        bkey = bkey > o.bkey ? bkey : o.bkey;
+        nan |= o.nan;
+        r.merge(o.r.m, o.r.s);
+        a += o.a;
+        b += o.b;
+    }
+    __device__ __forceinline__ Partial xor_lane(int mask) const {
+        Partial o;
+        o.key = shfl_x64(key, mask);
+        o.bkey = shfl_x64(bkey, mask);
+        o.nan = (uint32_t) __shfl_xor((int) nan, mask, 64);
+        o.r.m = shfl_x(r.m, mask);
+        o.r.s = shfl_x(r.s, mask);
+        o.a = shfl_x(a, mask);
+        o.b = shfl_x(b, mask);
+        return o;
+    }
+};
+
+__device__ __forceinline__ Partial wave_reduce(Partial p) {
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) p.merge(p.xor_lane(mask));
+    return p;  // (every lane holds the wave's result; the order of merges is fixed)
+}
+
+// A segment's record in the row's scratch: 8 words.
+__device__ __forceinline__ void put_rec(uint64_t* r, const Partial& p) {
+    const uint64_t w[8] = {p.key, p.bkey, p.nan, (uint64_t) __float_as_uint(p.r.m),
+                           (uint64_t) __double_as_longlong(p.r.s), (uint64_t) __double_as_longlong(p.a),
+                           (uint64_t) __double_as_longlong(p.b), 0ull};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) __hip_atomic_store(&r[i], w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ Partial get_rec(const uint64_t* r) {
+    uint64_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = __hip_atomic_load(&r[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Partial p;
+    p.key = w[0];
+    p.bkey = w[1];
+    p.nan = (uint32_t) w[2];
+    p.r.m = __uint_as_float((uint32_t) w[3]);
+    p.r.s = __longlong_as_double((long long) w[4]);
+    p.a = __longlong_as_double((long long) w[5]);
+    p.b = __longlong_as_double((long long) w[6]);
+    return p;
+}
+
+__shared__ uint64_t s_ppl[PPL_NW][8];
+__shared__ int s_ppl_last;
+
+__global__ __launch_bounds__(PPL_WG) void ppl_kernel(PplArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = blockIdx.x / a.segs, seg = blockIdx.x - row * a.segs;
+    const int lo = seg * a.seg_len, hi = min(a.V, lo + a.seg_len);
+    const float* __restrict__ L = a.logits + (int64_t) row * a.row_stride;
+    const float* __restrict__ B = a.base ? a.base + (int64_t) row * a.base_stride : nullptr;
+    Partial p;
+    // thread t reads ids lo + t, lo + t + WG, ... (coalesced; ascending per thread)
+    for (int id = lo + tid; id < hi; id += PPL_WG) {
+        const float x = L[id];
+        const uint64_t kx = num_key(x, id);
+        p.key = kx > p.key ? kx : p.key;
+        p.nan |= x != x ? 1u : 0u;
+        p.r.add(x);
+        if (B) {
+            const float b = B[id];
+            const uint64_t kb = num_key(b, id);
+            p.bkey = kb > p.bkey ? kb : p.bkey;
+            if (b > -16.0f) {
+                const double e = exp((double) b);
+                p.a += e * ((double) b - (double) x);
+                p.b += e;
+            }
+        }
+    }
+    p = wave_reduce(p);
+    if (lane == 0) {
+        uint64_t* r = &s_ppl[wave][0];
+        r[0] = p.key;
+        r[1] = p.bkey;
+        r[2] = p.nan;
+        r[3] = __float_as_uint(p.r.m);
+        r[4] = (uint64_t) __double_as_longlong(p.r.s);
+        r[5] = (uint64_t) __double_as_longlong(p.a);
+        r[6] = (uint64_t) __double_as_longlong(p.b);
+    }
+    __syncthreads();
+    uint64_t* rec = a.scratch + ((int64_t) row * a.segs + seg) * KCAP;
+    if (tid == 0) {
+        Partial q;
+        for (int w = 0; w < PPL_NW; ++w) {
+            Partial o;
+            o.key = s_ppl[w][0];
+            o.bkey = s_ppl[w][1];
+            o.nan = (uint32_t) s_ppl[w][2];
+            o.r.m = __uint_as_float((uint32_t) s_ppl[w][3]);
+            o.r.s = __longlong_as_double((long long) s_ppl[w][4]);
+            o.a = __longlong_as_double((long long) s_ppl[w][5]);
+            o.b = __longlong_as_double((long long) s_ppl[w][6]);
+            q.merge(o);
+        }
+        put_rec(rec, q);
+        // the record is acknowledged before the ticket: the last workgroup reads it after its own increment
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        const uint32_t prev = atomicAdd(&a.ticket[row], 1u);
+        s_ppl_last = prev == (uint32_t) (a.segs - 1);
+    }
+    __syncthreads();
+    if (!s_ppl_last || wave != 0) return;
+    // the row's last workgroup: wave 0 combines the segment records (lane s holds segment s, in a fixed order)
+    const uint64_t* recs = a.scratch + (int64_t) row * a.segs * KCAP;
+    Partial q;
+    for (int s0 = 0; s0 < a.segs; s0 += 64) {
+        Partial o;
+        if (s0 + lane < a.segs) o = get_rec(recs + (int64_t) (s0 + lane) * KCAP);
+        q.merge(wave_reduce(o));
+    }
+    if (lane != 0) return;
+    const float l0 = L[0];
+    const bool nan0 = l0 != l0;
+    const float mx = key_value(q.key);
+    double lse;
+    if (q.nan || q.key == 0ull || !(mx - mx == 0.0f))
+        lse = __longlong_as_double(0x7ff8000000000000ll);  // a NaN or an infinite maximum: the reference's NaN
+    else
+        lse = (double) mx + log(q.r.s * exp((double) q.r.m - (double) mx));
+    const int t = a.targets ? a.targets[row] : -1;
+    const bool tin = t >= 0 && t < a.V;
+    if (a.out_lse) a.out_lse[row] = lse;
+    if (a.out_nll) a.out_nll[row] = tin ? lse - (double) L[t] : __longlong_as_double(0x7ff8000000000000ll);
+    if (a.out_top) a.out_top[row] = (nan0 || q.key == 0ull) ? 0 : key_index(q.key);
+    if (B) {
+        const float b0 = B[0];
+        if (a.out_kl) a.out_kl[row] = q.b == 0.0 ? 0.0 : q.a + lse * q.b;  // (no term: the reference's 0)
+        if (a.out_base_top) a.out_base_top[row] = (b0 != b0 || q.bkey == 0ull) ? 0 : key_index(q.bkey);
+        if (a.out_nll_base) a.out_nll_base[row] = tin ? -(double) B[t] : __longlong_as_double(0x7ff8000000000000ll);
+    }
+    a.ticket[row] = 0u;  // (for the next launch)
+}
+
+}  // namespace
+
+int ppl_segments(int V, int rows, int* seg_len) {
+    // 256-thread workgroups over 2048..16384 ids: the longest whose grid still gives every CU a few
+    int sl = 16384;
+    while (sl > 2048 && (long long) rows * ((V + sl - 1) / sl) < 1024) sl >>= 1;
+    *seg_len = sl;
+    return (V + sl - 1) / sl;
+}
+
+hipError_t launch_ppl(const PplArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(ppl_kernel, dim3(a.n_rows * a.segs), dim3(PPL_WG), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace kls

@@ -152,6 +152,29 @@ class Sampler:
         _lib.check(_lib.lib().kls_argmax(self._h, _ptr(logits), rows, stride, _ptr(out), _stream_ptr(stream)),
                    "kls_argmax")
 
+    def ppl_scores(self, logits, targets, base=None, stream=None):
+        """cmd_ppl's per-token scores (src/main.cpp:308-327) for the device tensors logits [rows, V] f32 and
+        targets [rows] i32, optionally base log-probabilities [rows, V] f32. Returns device tensors: lse, nll
+        (f64), top (i32) and, with a base, kl, nll_base (f64) and base_top (i32). Asynchronous on `stream`."""
+        import torch
+        rows, n = int(logits.shape[0]), int(logits.shape[1])
+        self._ensure(n)
+        dev = logits.device
+        out = dict(lse=torch.empty(rows, dtype=torch.float64, device=dev),
+                   nll=torch.empty(rows, dtype=torch.float64, device=dev),
+                   top=torch.empty(rows, dtype=torch.int32, device=dev))
+        if base is not None:
+            out.update(kl=torch.empty(rows, dtype=torch.float64, device=dev),
+                       nll_base=torch.empty(rows, dtype=torch.float64, device=dev),
+                       base_top=torch.empty(rows, dtype=torch.int32, device=dev))
+        g = lambda k: _ptr(out[k]) if k in out else None
+        _lib.check(_lib.lib().kls_ppl_scores(
+            self._h, _ptr(logits), rows, int(logits.stride(0)), _ptr(targets),
+            None if base is None else _ptr(base), int(base.stride(0)) if base is not None else 0,
+            g("lse"), g("nll"), g("top"), g("kl"), g("nll_base"), g("base_top"), _stream_ptr(stream)),
+            "kls_ppl_scores")
+        return out
+
     def candidates(self, row: int = 0, cap: int = 64):
         """(ids, probs, k, kept) of the last call's row: the sorted top-k and softmax probabilities."""
         ids = np.zeros(cap, dtype=np.int32)

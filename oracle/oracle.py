@@ -75,6 +75,8 @@ def lib():
         L.orc_expf_compare.argtypes = [C.c_uint32, C.POINTER(C.c_float), C.c_longlong, C.c_int,
                                        C.POINTER(C.c_uint32)]
         L.orc_time_rows.restype = C.c_double
+        L.orc_ppl_row.argtypes = [C.POINTER(C.c_float), C.c_int, C.c_int, C.POINTER(C.c_float),
+                                  C.POINTER(C.c_double), C.POINTER(C.c_int32)]
         L.orc_argmax.argtypes = [C.POINTER(C.c_float), C.c_int]
         L.orc_argmax.restype = C.c_int32
         L.orc_time_rows.argtypes = [C.POINTER(C.c_float), C.c_int, C.c_int, C.POINTER(OrcParams),
@@ -154,6 +156,20 @@ def verify(logits: np.ndarray, drafts: np.ndarray, p, u: np.ndarray, counts: np.
     acc = lib().orc_verify(_fp(lg), V, nb, _ip(dr) if dr.size else None, C.byref(ps),
                            None if cnt is None else _ip(cnt), _dp(uu), mode, _ip(toks))
     return toks, int(acc), cnt
+
+
+def ppl_row(logits_row: np.ndarray, target: int, base: np.ndarray | None = None) -> dict:
+    """Per-token scoring of cmd_ppl (src/main.cpp:308-327): lse, nll, imax and, with base log-probabilities,
+    kl, nll_base, ibase."""
+    r = np.ascontiguousarray(logits_row, dtype=np.float32)
+    b = None if base is None else np.ascontiguousarray(base, dtype=np.float32)
+    out = np.zeros(4, dtype=np.float64)
+    tops = np.zeros(2, dtype=np.int32)
+    lib().orc_ppl_row(_fp(r), int(r.shape[0]), int(target), None if b is None else _fp(b), _dp(out), _ip(tops))
+    d = dict(lse=float(out[0]), nll=float(out[1]), top=int(tops[0]))
+    if b is not None:
+        d.update(kl=float(out[2]), nll_base=float(out[3]), base_top=int(tops[1]))
+    return d
 
 
 def argmax(row: np.ndarray) -> int:

@@ -18,6 +18,8 @@
 //   orc_uniforms         : C++ standard KAT (10000th output of mt19937_64 = 9981545732273789042) and the
 //                          reference's own draws (oracle/_ref with the same seed).
 //   orc_expf_glibc       : exhaustive comparison against the host libm expf over every float in [-110, 89].
+//   orc_ppl_row          : closed forms in float64 (numpy logsumexp and the KL sum) to rounding, the first-maximum
+//                          rule on planted ties, and the NaN / infinity cases (tests/test_oracle.py).
 //   orc_argmax           : the library call itself (std::max_element, as engine.cpp:414); checked against the
 //                          textbook loop on small rows and the closed form (first index of the largest value
 //                          among numbers; a NaN first element wins) on planted ties, NaNs and infinities.
@@ -325,6 +327,36 @@ long long orc_expf_compare(uint32_t lo, const float* gpu, long long n, int nthre
     }
     if (first_bad) *first_bad = (uint32_t) (f == UINT64_MAX ? 0 : f);
     return total;
+}
+
+// The per-token scoring of cmd_ppl (src/main.cpp:308-327) for one row of logits with target `target`:
+// out[0] = lse, out[1] = nll, and with a base row of log-probabilities (nullable) out[2] = kl, out[3] = base
+// nll; tops[0] = imax, tops[1] = ibase. Same operations, types and order as the reference loop.
+void orc_ppl_row(const float* l, int n_vocab, int target, const float* blp, double* out, int32_t* tops) {
+    float mx = l[0];  // main.cpp:308-311
+    int imax = 0;
+    for (int v = 1; v < n_vocab; ++v)
+        if (l[v] > mx) {
+            mx = l[v];
+            imax = v;
+        }
+    double sum = 0.0;  // :312-313
+    for (int v = 0; v < n_vocab; ++v) sum += std::exp((double) l[v] - mx);
+    const double lse = mx + std::log(sum);  // :314
+    out[0] = lse;
+    out[1] = lse - l[target];  // :315
+    tops[0] = imax;
+    if (blp) {
+        out[3] = -blp[target];  // :319
+        double kl = 0.0;        // :320-325
+        int ibase = 0;
+        for (int v = 0; v < n_vocab; ++v) {
+            if (blp[v] > blp[ibase]) ibase = v;
+            if (blp[v] > -16.0f) kl += std::exp((double) blp[v]) * (blp[v] - (l[v] - lse));
+        }
+        out[2] = kl;
+        tops[1] = ibase;
+    }
 }
 
 // Engine::mtp_draft_token (src/engine.cpp:413-415): the index std::max_element returns over one row.

@@ -179,6 +179,55 @@ def test_argmax_matches_textbook_loop_and_closed_form(oracle_lib):
     assert oracle_lib.argmax(np.array([-np.inf, np.nan, -np.inf], np.float32)) == 0
 
 
+def _ppl_closed(l, t, b=None):
+    """Float64 closed forms of the ppl scores: numpy's (pairwise) sums instead of the loop's sequential ones."""
+    x = l.astype(np.float64)
+    mx = float(l[0]) if np.isnan(l[0]) else float(np.nanmax(np.where(np.isnan(l), -np.inf, l)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        lse = mx + np.log(np.sum(np.exp(x - mx)))
+    d = dict(lse=lse, nll=lse - x[t], top=_max_element_closed(l))
+    if b is not None:
+        bb = b.astype(np.float64)
+        m = b > -16.0
+        terms = np.exp(bb[m]) * (bb[m] - (x[m] - lse))
+        d.update(kl=float(np.sum(terms)), kl_mag=float(np.sum(np.abs(terms))), nll_base=-bb[t],
+                 base_top=_max_element_closed(b))
+    return d
+
+
+def test_ppl_row_closed_forms(oracle_lib):
+    """cmd_ppl's per-token scores (main.cpp:308-327): lse and nll against float64 logsumexp, kl against the
+    float64 sum of its terms, both to rounding (a float exp, a dropped term or a sign error is far outside), the
+    indices by the first-maximum rule, and the NaN / infinity outcomes."""
+    rng = np.random.default_rng(21)
+    for trial in range(12):
+        V = int(rng.integers(2, 60000))
+        l = (rng.standard_normal(V) * 2).astype(np.float32)
+        l[rng.integers(0, V, 3)] = l.max()  # ties with the maximum
+        z = (rng.standard_normal(V) * 3).astype(np.float64)
+        b = (z - (z.max() + np.log(np.sum(np.exp(z - z.max()))))).astype(np.float32)  # base log-probabilities
+        t = int(rng.integers(0, V))
+        got = oracle_lib.ppl_row(l, t, b)
+        exp = _ppl_closed(l, t, b)
+        assert got["top"] == exp["top"] and got["base_top"] == exp["base_top"]
+        assert abs(got["lse"] - exp["lse"]) <= 1e-12 * abs(exp["lse"]) + 1e-13
+        assert abs(got["nll"] - exp["nll"]) <= 1e-12 * abs(exp["lse"]) + 1e-13
+        assert abs(got["kl"] - exp["kl"]) <= 1e-12 * exp["kl_mag"] + 1e-15
+        assert got["nll_base"] == exp["nll_base"]
+    # NaN and infinities: the reference's arithmetic decides
+    nan = np.float32(np.nan)
+    r = oracle_lib.ppl_row(np.array([nan, 1, 2], np.float32), 1)
+    assert np.isnan(r["lse"]) and r["top"] == 0
+    r = oracle_lib.ppl_row(np.array([0, nan, 2], np.float32), 1)
+    assert np.isnan(r["lse"]) and r["top"] == 2
+    r = oracle_lib.ppl_row(np.array([-np.inf, -np.inf], np.float32), 0)
+    assert np.isnan(r["lse"]) and r["top"] == 0
+    r = oracle_lib.ppl_row(np.array([1, np.inf, 2], np.float32), 0)
+    assert np.isnan(r["lse"]) and r["top"] == 1
+    r = oracle_lib.ppl_row(np.array([-np.inf, 0.0, 0.0], np.float32), 1)
+    assert r["lse"] == np.log(2.0) and r["top"] == 1 and r["nll"] == np.log(2.0)
+
+
 def test_penalty_closed_form_brute_force(oracle_lib):
     """Tiny vocabulary: greedy over the penalized logits written out with explicit float32 roundings."""
     rng = np.random.default_rng(11)
