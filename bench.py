@@ -15,6 +15,10 @@ Also reported:
                 presence 0.5, frequency 0.2), top-k 64, top-p 0.9: device time per batch (history partition +
                 sampling kernels, back-to-back launches), hot (same input every launch) and cold (8 input sets
                 rotated, 509 MB, more than the 256 MB last-level cache);
+  next_rows     the MTP draft argmax (Engine::mtp_draft_token, 1 row x 248,320: std::max_element) per call, and
+                one pass of the perplexity / KL loop (src/main.cpp:308-327: 64 rows x 248,320 logits plus base
+                log-probabilities) per pass, cold (4 input sets rotated), with their HBM rates (device time
+                of launches captured back to back in one graph);
   cpu_baseline  the reference's own sampler.cpp (oracle/_ref, built -O3 from its sources) on one host core,
                 4 rows per step, over a bounded sample.
 """
@@ -44,6 +48,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--no-next", action="store_true", help="skip the draft-argmax and ppl measurements")
     return ap.parse_args()
 
 
@@ -78,6 +83,76 @@ def copy_probe(torch, stream):
     del a, b
     return {"bytes_read": n * 4, "bytes_written": n * 4, "us": round(us, 2),
             "GBps_read_plus_write": round(2 * n * 4 / (us * 1e-6) / 1e9, 1)}
+
+
+def graph_us(torch, launch, n):
+    """Device µs per launch: n launches captured in one graph (no host work between them), the replay timed
+    with stream events. launch(stream_ptr) enqueues one call on the given stream."""
+    import ctypes as C
+    cs = torch.cuda.Stream()
+    launch(C.c_void_p(cs.cuda_stream))  # (first call outside the capture)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        for _ in range(n):
+            launch(C.c_void_p(cs.cuda_stream))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 5
+    with torch.cuda.stream(cs):  # (replays run on the current stream)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        e0.record(cs)
+        for _ in range(reps):
+            g.replay()
+        e1.record(cs)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * n)
+
+
+def next_rows(torch, klein_amd, W):
+    import ctypes as C
+    import numpy as np
+    from klein_amd import _lib
+    L = _lib.lib()
+    rng = np.random.default_rng(77)
+    res = {}
+    S = klein_amd.Sampler(W.Params(temperature=0.0), n_vocab=V, max_rows=64)
+    h = S._h
+    p = lambda t: C.c_void_p(t.data_ptr())
+    # draft argmax: one MTP row (the greedy workload's logits), as called once per draft
+    g = W.greedy()
+    d1 = torch.from_numpy(g.logits).cuda()
+    o1 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    us = graph_us(torch, lambda sp: _lib.check(L.kls_argmax(h, p(d1), 1, V, p(o1), sp), "kls_argmax"), 200)
+    assert int(o1.item()) == g.expected_greedy
+    res["draft_argmax"] = {"workload": "1 row x 248,320 f32 (std::max_element)", "us": round(us, 2),
+                           "GBps": round(V * 4 / (us * 1e-6) / 1e9, 1)}
+    # ppl: the loop's default pass of 64 rows with a KL base, 4 input sets (254 MB each way) rotated
+    sets = []
+    for j in range(4):
+        x = torch.randn((64, V), device="cuda", dtype=torch.float32) * 2.0
+        b = torch.log_softmax(torch.randn((64, V), device="cuda", dtype=torch.float32) * 3.0, dim=1)
+        sets.append((x, b))
+    tg = torch.from_numpy(rng.integers(0, V, 64).astype(np.int32)).cuda()
+    outs = [torch.empty(64, dtype=torch.float64, device="cuda") for _ in range(4)]
+    tops = [torch.empty(64, dtype=torch.int32, device="cuda") for _ in range(2)]
+    k = [0]
+
+    def ppl(sp):
+        x, b = sets[k[0] % 4]
+        k[0] += 1
+        _lib.check(L.kls_ppl_scores(h, p(x), 64, V, p(tg), p(b), V, p(outs[0]), p(outs[1]), p(tops[0]),
+                                    p(outs[2]), p(outs[3]), p(tops[1]), sp), "kls_ppl_scores")
+
+    us = graph_us(torch, ppl, 40)
+    pbytes = 2 * 64 * V * 4 + 64 * 4
+    res["ppl_pass"] = {"workload": "64 rows x 248,320 logits + base log-probabilities, per-token lse/nll/KL",
+                       "algorithmic_bytes": pbytes, "us_cold": round(us, 2),
+                       "GBps": round(pbytes / (us * 1e-6) / 1e9, 1),
+                       "frac": round(pbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    S.close()
+    return res
 
 
 def cpu_baseline(w, seconds):
@@ -247,6 +322,10 @@ def main():
                           "frac_cold": round(BATCH_BYTES / (res["cold"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                           "GBps_hot": round(BATCH_BYTES / (res["hot"] * 1e-6) / 1e9, 1)}
         SB.close()
+
+    # ---------------- the next rows of the path: draft argmax, ppl scoring
+    if not a.no_next:
+        out["next_rows"] = next_rows(torch, klein_amd, W)
 
     out["copy_probe"] = copy_probe(torch, stream)
     if not a.no_cpu:

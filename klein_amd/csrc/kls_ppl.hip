@@ -37,17 +37,51 @@ __device__ __forceinline__ float key_value(uint64_t k) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
 }
 
+// exp in double for the sums, by Tang's table-driven method (ACM TOMS 15(2), 1989): k = rint(x*64/ln2),
+// r = x - k*ln2/64 (a 36-bit leading part of ln2/64, so k times it is exact, plus the remainder), and
+// exp(x) = 2^(k>>6) * 2^((k&63)/64) * exp(r), with 2^(j/64) from a table of the correctly rounded values and
+// exp(r) - 1 by its Taylor polynomial to r^6 (|r| <= ln2/128, so the next term is below 3e-20). About one ulp.
+// x is clamped to [-800, 710] (results 0 and inf there, as exp's); the callers never pass NaN.
+__device__ const double kExp64Tab[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0};
+
+__device__ __forceinline__ double exp_tab(double x, const double* tab) {
+    x = fmin(fmax(x, -800.0), 710.0);
+    const double kd = __builtin_rint(x * 0x1.71547652b82fep+6);
+    const double r = fma(-kd, 0x1.cf79abc9e3b3ap-46, fma(-kd, 0x1.62e42fefa0000p-7, x));
+    const int k = (int) kd;
+    const double q = fma(r, fma(r, fma(r, fma(r, 1.0 / 720, 1.0 / 120), 1.0 / 24), 1.0 / 6), 0.5);
+    const double p = fma(r * r, q, r);
+    const double t = tab[k & 63];
+    return ldexp(fma(t, p, t), k >> 6);
+}
+
 // A running maximum m of the finite logits seen and s = sum over them of exp(x - m).
 struct RunSum {
     float m = -INFINITY;
     double s = 0.0;
-    __device__ __forceinline__ void add(float x) {
+    __device__ __forceinline__ void add(float x, const double* tab) {
         if (!(x - x == 0.0f)) return;  // NaN and infinities are accounted for by the flags
         if (x > m) {
-            s = s * exp((double) m - (double) x);  // (0 while m is -inf)
+            s = s * exp_tab((double) m - (double) x, tab);  // (0 while m is -inf: the clamp gives exp(-800))
             m = x;
         }
-        s += exp((double) x - (double) m);
+        s += exp_tab((double) x - (double) m, tab);
     }
     __device__ __forceinline__ void merge(float m2, double s2) {
         const float mm = fmaxf(m, m2);
@@ -126,6 +160,7 @@ __device__ __forceinline__ Partial get_rec(const uint64_t* r) {
 }
 
 __shared__ uint64_t s_ppl[PPL_NW][8];
+__shared__ double s_exp64[64];
 __shared__ int s_ppl_last;
 
 __global__ __launch_bounds__(PPL_WG) void ppl_kernel(PplArgs a) {
@@ -134,25 +169,81 @@ __global__ __launch_bounds__(PPL_WG) void ppl_kernel(PplArgs a) {
     const int lo = seg * a.seg_len, hi = min(a.V, lo + a.seg_len);
     const float* __restrict__ L = a.logits + (int64_t) row * a.row_stride;
     const float* __restrict__ B = a.base ? a.base + (int64_t) row * a.base_stride : nullptr;
+    if (tid < 64) s_exp64[tid] = kExp64Tab[tid];
+    __syncthreads();
     Partial p;
-    // thread t reads ids lo + t, lo + t + WG, ... (coalesced; ascending per thread)
-    for (int id = lo + tid; id < hi; id += PPL_WG) {
-        const float x = L[id];
-        const uint64_t kx = num_key(x, id);
-        p.key = kx > p.key ? kx : p.key;
-        p.nan |= x != x ? 1u : 0u;
-        p.r.add(x);
+    // Thread t holds ids s0 + e (e < 4) of each step, s0 = lo + 4*(t + j*WG): float4 loads when the rows are
+    // 16-byte aligned. Per thread the ids ascend, so the first maximum is kept with a strict '>'. The running
+    // maximum moves once per step (its rescaling exp is not per logit), and excluded or non-finite terms enter
+    // as exp of the clamp, 0.
+    const bool vec = ((reinterpret_cast<uintptr_t>(L) | (B ? reinterpret_cast<uintptr_t>(B) : 0)) & 15u) == 0;
+    float bx = -INFINITY, bb = -INFINITY;  // first maxima (logits, base) and their ids (INT_MAX: none yet)
+    int ix = 0x7fffffff, ib = 0x7fffffff;
+    // one float4 of each row per thread and step, the next step's loads issued before this step's work
+    auto load = [&](int i0, float (&xv)[4], float (&bv)[4]) {
+        if (vec && i0 + 3 < hi) {
+            const float4 q = *reinterpret_cast<const float4*>(L + i0);
+            xv[0] = q.x, xv[1] = q.y, xv[2] = q.z, xv[3] = q.w;
+            if (B) {
+                const float4 r = *reinterpret_cast<const float4*>(B + i0);
+                bv[0] = r.x, bv[1] = r.y, bv[2] = r.z, bv[3] = r.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool in = i0 + e < hi;
+                xv[e] = in ? L[i0 + e] : -INFINITY;
+                if (B) bv[e] = in ? B[i0 + e] : -INFINITY;
+            }
+        }
+    };
+    float xn[4], bn[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    load(lo + 4 * tid, xn, bn);
+    for (int s0 = lo + 4 * tid; s0 - 4 * tid < hi; s0 += 4 * PPL_WG) {
+        float xv[4], bv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = xn[e], bv[e] = bn[e];
+        if (s0 + 4 * PPL_WG - 4 * tid < hi) load(s0 + 4 * PPL_WG, xn, bn);
+        float cm = p.r.m;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int id = s0 + e;
+            const bool in = id < hi;
+            const float x = xv[e];
+            if (in && (x > bx || (ix == 0x7fffffff && x == bx))) {
+                bx = x;
+                ix = id;
+            }
+            p.nan |= (in && x != x) ? 1u : 0u;
+            if (x - x == 0.0f) cm = fmaxf(cm, x);  // (out-of-segment slots are -inf)
+        }
+        if (cm > p.r.m) {
+            p.r.s = p.r.s * exp_tab((double) p.r.m - (double) cm, s_exp64);
+            p.r.m = cm;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x = xv[e];
+            p.r.s += exp_tab(x - x == 0.0f ? (double) x - (double) p.r.m : -800.0, s_exp64);
+        }
         if (B) {
-            const float b = B[id];
-            const uint64_t kb = num_key(b, id);
-            p.bkey = kb > p.bkey ? kb : p.bkey;
-            if (b > -16.0f) {
-                const double e = exp((double) b);
-                p.a += e * ((double) b - (double) x);
-                p.b += e;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int id = s0 + e;
+                const float b = bv[e], x = xv[e];
+                if (id < hi && (b > bb || (ib == 0x7fffffff && b == bb))) {
+                    bb = b;
+                    ib = id;
+                }
+                const bool term = id < hi && b > -16.0f;
+                const double eb = exp_tab(term ? (double) b : -800.0, s_exp64);
+                p.a += term ? eb * ((double) b - (double) x) : 0.0;
+                p.b += eb;
             }
         }
     }
+    p.key = ix == 0x7fffffff ? 0ull : num_key(bx, ix);
+    p.bkey = ib == 0x7fffffff ? 0ull : num_key(bb, ib);
     p = wave_reduce(p);
     if (lane == 0) {
         uint64_t* r = &s_ppl[wave][0];
