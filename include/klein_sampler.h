@@ -129,6 +129,13 @@ int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int ca
  * exponential with the host libm's std::exp(float) (src/sampler.cpp:57) over whole ranges of inputs. */
 int kls_debug_expf(uint32_t lo, long long n, float* d_out, kls_stream stream);
 
+/* Test hook, no counterpart in the reference: the wide top-k tail's parallel replay of a sequential double sum
+ * (src/sampler.cpp:58,70-77,84-87 accumulate this way) over the n device doubles d_terms from acc0:
+ * acc = acc + d_terms[i] in order, stopping after the first i where (mode 1) acc >= thr or (mode 2) acc <= 0
+ * (mode 0: never). d_out[0] receives the result, d_out[1] the stop index (-1: none). Asynchronous on `stream`. */
+int kls_debug_sum_replay(const double* d_terms, int n, double acc0, int mode, double thr, double* d_out,
+                         kls_stream stream);
+
 /* Human-readable name of a status code. */
 const char* kls_status_string(int status);
 

@@ -2,7 +2,7 @@
 min-p/top-p, the seeded draw (src/sampler.cpp) and the MTP verify accept rule (src/engine.cpp:563-575), as HIP
 kernels behind the C ABI of include/klein_sampler.h."""
 from .workloads import Params, VOCAB  # noqa: F401
-from .sampler import Sampler, debug_expf  # noqa: F401
+from .sampler import Sampler, debug_expf, debug_sum_replay  # noqa: F401
 from . import _lib  # noqa: F401
 
 

@@ -20,7 +20,7 @@ KLS_ERR_OOM = 6
 # every entry point include/klein_sampler.h declares
 EXPORTS = ["kls_create", "kls_destroy", "kls_reset", "kls_accept", "kls_sample", "kls_verify", "kls_verify_enqueue",
            "kls_verify_wait", "kls_sample_batch", "kls_argmax", "kls_ppl_scores",
-           "kls_get_candidates", "kls_debug_expf", "kls_status_string", "kls_last_error"]
+           "kls_get_candidates", "kls_debug_expf", "kls_debug_sum_replay", "kls_status_string", "kls_last_error"]
 
 
 class KlsParams(C.Structure):
@@ -62,6 +62,8 @@ def lib():
                                      C.c_void_p]
         L.kls_get_candidates.argtypes = [P, C.c_int, I32P, F32P, C.c_int, I32P, I32P]
         L.kls_debug_expf.argtypes = [C.c_uint32, C.c_longlong, C.c_void_p, C.c_void_p]
+        L.kls_debug_sum_replay.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_int, C.c_double, C.c_void_p,
+                                           C.c_void_p]
         L.kls_status_string.restype = C.c_char_p
         L.kls_status_string.argtypes = [C.c_int]
         L.kls_last_error.restype = C.c_char_p

@@ -604,6 +604,13 @@ int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int ca
     return KLS_OK;
 }
 
+int kls_debug_sum_replay(const double* d_terms, int n, double acc0, int mode, double thr, double* d_out,
+                         kls_stream stream) {
+    if ((!d_terms && n > 0) || !d_out || n < 0 || mode < 0 || mode > 2) return fail(KLS_ERR_INVALID_ARG, "bad arguments");
+    KLS_HIP(launch_sum_replay(d_terms, n, acc0, mode, thr, d_out, (hipStream_t) stream));
+    return KLS_OK;
+}
+
 // Test hook: expf of the consecutive float bit patterns lo, lo+1, ... (n of them) into device memory `out`.
 int kls_debug_expf(uint32_t lo, long long n, float* out, kls_stream stream) {
     if (!out || n < 0) return fail(KLS_ERR_INVALID_ARG, "bad arguments");

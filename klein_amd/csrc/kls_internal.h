@@ -142,6 +142,8 @@ hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_
 int rows_grid(const RowsArgs& a);  // workgroups launch_rows starts
 hipError_t prepare_rows_kernels();  // once per device: LDS limits of the kernels with large count tables
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s);
+// Test hook of the wide tail's exact sum replay (see kls_debug_sum_replay).
+hipError_t launch_sum_replay(const double* t, int n, double acc0, int mode, double thr, double* out, hipStream_t s);
 // Wide top-k: keys (with penalties from the history in `a`), the sort, the tail (tokens published as
 // launch_rows does).
 hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipStream_t s);

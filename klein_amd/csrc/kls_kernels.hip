@@ -1395,36 +1395,168 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
 // candidate order, run by wave 0 over 64-candidate chunks (lane j holding candidate c + j) with the loads of the
 // next chunks in flight.
 constexpr int TAIL_WG = 1024;
-constexpr int TAIL_AHEAD = 4;  // chunks loaded ahead of the chain
+__shared__ int s_wide_n;  // kk, then the min-p length
 
-__shared__ int s_wide_n;    // kk, then the min-p length
-__shared__ double s_wide_sum;
+// ---- Exact parallel replay of a sequential double sum: acc <- RN(acc + t_i), i = 0, 1, ... in order.
+// While acc > 0 stays in one binade [2^E, 2^(E+1)) every value on the way is A * u with u = 2^(E-52) and A an
+// integer in [2^52, 2^53), and RN(A*u + t) = (A + d)*u where, writing t/u = f + phi (f integer, 0 <= phi < 1),
+// d = f when phi < 1/2, f + 1 when phi > 1/2, and at a tie (phi = 1/2) whichever of f, f + 1 makes A + d even.
+// So each term is a map of the parity of A: (d for parity 0, d for parity 1, parity after each). Maps compose
+// associatively, so a workgroup scans 1,024 terms at a time and knows every A on the way. A term whose exact
+// sum could leave the binade (A + f < 2^52, or A + f >= 2^53 - 1, or t/u huge) is added with the real double
+// addition instead, and the scan restarts after it in the new binade; so is every term while acc is 0 or
+// subnormal. Identical results to the sequential loop, in ~250 workgroup steps for 248,320 terms.
+struct ParMap {
+    long long d0, d1;  // increments (in units of u) for incoming parity 0 / 1
+    uint32_t p;        // bit 0: parity after, from parity 0; bit 1: from parity 1
+};
 
-// Sequential double chain over terms t[0..n) (wave 0): f(acc, i, term) returns false to stop after term i.
+__device__ __forceinline__ ParMap par_identity() { return ParMap{0, 0, 2u}; }
+
+// e first, then l
+__device__ __forceinline__ ParMap par_compose(const ParMap& e, const ParMap& l) {
+    const uint32_t e0 = e.p & 1u, e1 = (e.p >> 1) & 1u, l0 = l.p & 1u, l1 = (l.p >> 1) & 1u;
+    ParMap c;
+    c.d0 = e.d0 + (e0 ? l.d1 : l.d0);
+    c.d1 = e.d1 + (e1 ? l.d1 : l.d0);
+    c.p = (e0 ? l1 : l0) | ((e1 ? l1 : l0) << 1);
+    return c;
+}
+
+__device__ __forceinline__ long long shfl_up_ll(long long v, int d) {
+    const int lo = __shfl_up((int) (unsigned long long) v, (unsigned) d, 64);
+    const int hi = __shfl_up((int) ((unsigned long long) v >> 32), (unsigned) d, 64);
+    return (long long) (((unsigned long long) (unsigned) hi << 32) | (unsigned) lo);
+}
+
+__device__ __forceinline__ ParMap shfl_up_map(const ParMap& m, int d) {
+    return ParMap{shfl_up_ll(m.d0, d), shfl_up_ll(m.d1, d), (uint32_t) __shfl_up((int) m.p, (unsigned) d, 64)};
+}
+
+__shared__ ParMap s_rp_wave[TAIL_WG / 64];
+__shared__ int s_rp_first;
+__shared__ double s_rp_acc;
+__shared__ int s_rp_next, s_rp_stop;
+
+// Replays the chain over t[0..n) from `acc` with the whole workgroup (every thread calls it, uniformly);
+// stop(acc, i) is evaluated on each partial result after term i, and the first i for which it holds ends the
+// chain (returned in *stopped, else -1). Returns the last partial result.
 template <typename F>
-__device__ __forceinline__ double chain(const double* __restrict__ t, int n, double acc, int lane, F f) {
-    double nxt[TAIL_AHEAD];
-#pragma unroll
-    for (int q = 0; q < TAIL_AHEAD; ++q) nxt[q] = (64 * q + lane < n) ? t[64 * q + lane] : 0.0;
-    for (int c = 0; c < n; c += 64 * TAIL_AHEAD) {
-        double cur[TAIL_AHEAD];
-#pragma unroll
-        for (int q = 0; q < TAIL_AHEAD; ++q) {
-            cur[q] = nxt[q];
-            const int i = c + 64 * (TAIL_AHEAD + q) + lane;
-            nxt[q] = i < n ? t[i] : 0.0;
+__device__ double replay_sum(const double* __restrict__ t, int n, double acc, F stop, int* stopped) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr long long TWO52 = 1ll << 52, TWO53 = 1ll << 53;
+    int i = 0, st = -1;
+    while (i < n) {
+        if (!(acc >= 0x1p-1000 && acc <= 0x1.fffffffffffffp+1023)) {
+            // zero, negative, subnormal, tiny, infinite or NaN: one real addition (every thread the same)
+            acc = __dadd_rn(acc, t[i]);
+            if (stop(acc, i)) {
+                st = i;
+                break;
+            }
+            ++i;
+            continue;
         }
-#pragma unroll
-        for (int q = 0; q < TAIL_AHEAD; ++q) {
-            const int c0 = c + 64 * q;
-            const int nv = min(64, n - c0);
-            for (int j = 0; j < nv; ++j) {
-                acc = __dadd_rn(acc, rdlaned(cur[q], j));
-                if (!f(acc, c0 + j)) return acc;
+        int E;
+        (void) frexp(acc, &E);  // acc in [2^(E-1), 2^E)
+        E -= 1;
+        const double u = ldexp(1.0, E - 52);
+        const long long A0 = (long long) ldexp(acc, 52 - E);
+        const uint32_t pi0 = (uint32_t) (A0 & 1);
+        const int j = i + tid;
+        const bool in = j < n;
+        const double tj = in ? t[j] : 0.0;
+        const double q = ldexp(tj, 52 - E);
+        bool cross = false;
+        long long f = 0;
+        ParMap m = par_identity();
+        if (in) {
+            if (!(fabs(q) < 0x1p62)) {
+                cross = true;  // (handled by the real addition; the map is not used past it)
+            } else {
+                const double fl = floor(q);
+                f = (long long) fl;
+                const double ph = q - fl;  // exact
+                if (ph == 0.5) {
+                    m.d0 = f + (f & 1);
+                    m.d1 = f + ((f + 1) & 1);
+                    m.p = 0u;
+                } else {
+                    const long long d = f + (ph > 0.5 ? 1 : 0);
+                    m.d0 = m.d1 = d;
+                    m.p = (uint32_t) (d & 1) | ((uint32_t) ((d + 1) & 1) << 1);
+                }
             }
         }
+        // workgroup inclusive scan of the maps (waves, then the waves' totals)
+        ParMap x = m;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const ParMap y = shfl_up_map(x, d);
+            if (lane >= d) x = par_compose(y, x);
+        }
+        ParMap xe = shfl_up_map(x, 1);
+        if (lane == 0) xe = par_identity();
+        if (lane == 63) s_rp_wave[wave] = x;
+        if (tid == 0) s_rp_first = 0x7fffffff;
+        __syncthreads();
+        ParMap pre = par_identity();
+        for (int w2 = 0; w2 < wave; ++w2) pre = par_compose(pre, s_rp_wave[w2]);
+        const ParMap X = par_compose(pre, xe);  // the terms before j in this block
+        const long long Aj = A0 + (pi0 ? X.d1 : X.d0);
+        const uint32_t pij = pi0 ? ((X.p >> 1) & 1u) : (X.p & 1u);
+        const long long dj = pij ? m.d1 : m.d0;
+        if (in && !cross) cross = (Aj + f < TWO52) || (Aj + f >= TWO53 - 1);
+        const double nxt = (double) (Aj + dj) * u;  // (exact when no earlier term crossed)
+        const bool hit = in && (cross || stop(nxt, j));
+        if (hit) atomicMin(&s_rp_first, j - i);
+        __syncthreads();
+        const int first = s_rp_first;
+        if (first == 0x7fffffff) {
+            // no term left the binade or stopped: the block's total
+            ParMap tot = par_identity();
+            for (int w2 = 0; w2 < TAIL_WG / 64; ++w2) tot = par_compose(tot, s_rp_wave[w2]);
+            acc = (double) (A0 + (pi0 ? tot.d1 : tot.d0)) * u;
+            i += TAIL_WG;
+        } else {
+            if (tid == first) {
+                double r;
+                int nx = j + 1, s2 = -1;
+                if (cross) {
+                    r = __dadd_rn((double) Aj * u, tj);
+                    if (stop(r, j)) s2 = j;
+                } else {
+                    r = nxt;
+                    s2 = j;
+                }
+                s_rp_acc = r;
+                s_rp_next = nx;
+                s_rp_stop = s2;
+            }
+            __syncthreads();
+            acc = s_rp_acc;
+            i = s_rp_next;
+            st = s_rp_stop;
+            if (st >= 0) break;
+        }
+        __syncthreads();  // (the LDS words are rewritten by the next block)
     }
+    *stopped = st;
     return acc;
+}
+
+// Test hook: replay_sum over t[0..n) from acc0; mode 0 never stops, 1 stops at acc >= thr, 2 at acc <= 0.
+// out[0] = the result, out[1] = the stop index (-1: none).
+__global__ __launch_bounds__(TAIL_WG) void sum_replay_kernel(const double* t, int n, double acc0, int mode, double thr,
+                                                             double* out) {
+    int st;
+    const double r = replay_sum(t, n, acc0, [mode, thr](double acc, int) {
+        return mode == 1 ? acc >= thr : mode == 2 ? acc <= 0.0 : false;
+    }, &st);
+    if (threadIdx.x == 0) {
+        out[0] = r;
+        out[1] = (double) st;
+    }
 }
 
 __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs w) {
@@ -1462,13 +1594,9 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
     }
     __syncthreads();
     const int kk = s_wide_n;
-    // the softmax total (:58), sequential
-    if (wave == 0) {
-        const double sum = chain(t, kk, 0.0, lane, [](double, int) { return true; });
-        if (lane == 0) s_wide_sum = sum;
-    }
-    __syncthreads();
-    const double sum = s_wide_sum;
+    // the softmax total (:58), in reference order (exact replay)
+    int st;
+    const double sum = replay_sum(t, kk, 0.0, [](double, int) { return false; }, &st);
     // p_i (:60), and min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
     const double e0 = (double) expf_glibc(__fdiv_rn(__fsub_rn(maxl, maxl), p.temperature));
     const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
@@ -1480,41 +1608,28 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
         t[i] = (double) pi;
     }
     __syncthreads();
-    if (wave != 0) return;
     int n = s_wide_n;
     // top-p (:69-79): cum over the candidates until it reaches top_p; the draw total (:80-81) is the same chain
     // over the kept ones
     double total;
     if (p.top_p < 1.0f) {
-        int m = n;
         const double tp = (double) p.top_p;
-        total = chain(t, n, 0.0, lane, [&](double acc, int i) {
-            if (acc >= tp) {
-                m = i + 1;
-                return false;
-            }
-            return true;
-        });
-        n = max(m, 1);
+        total = replay_sum(t, n, 0.0, [tp](double acc, int) { return acc >= tp; }, &st);
+        n = st >= 0 ? st + 1 : n;
     } else {
-        total = chain(t, n, 0.0, lane, [](double, int) { return true; });
+        total = replay_sum(t, n, 0.0, [](double, int) { return false; }, &st);
     }
     // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a chain
     // of additions of -p_i (exactly the subtractions)
     const double r0 = __dadd_rn(__dmul_rn(a.u[row], __dsub_rn(total, 0.0)), 0.0);
     const bool act = lane < kk;
     const float dbg_p = act ? (float) t[lane] : 0.0f;
-    int idx = n - 1;
-    for (int c = 0; c < n; c += 64) {  // (p_i negated in place for the chain)
-        if (c + lane < n) t[c + lane] = -t[c + lane];
-    }
-    chain(t, n, r0, lane, [&](double r, int i) {
-        if (r <= 0.0) {
-            idx = i;
-            return false;
-        }
-        return true;
-    });
+    __syncthreads();  // (every thread has read its p_i for the debug copy)
+    for (int i = tid; i < n; i += TAIL_WG) t[i] = -t[i];  // (p_i negated in place for the chain)
+    __syncthreads();
+    replay_sum(t, n, r0, [](double r, int) { return r <= 0.0; }, &st);
+    const int idx = st >= 0 ? st : n - 1;
+    if (wave != 0) return;
     const int tok = (int) (~(uint32_t) K[idx] & idm);
     const uint32_t ol = act ? img(lane) : 0u;
     if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = act ? ((uint64_t) ol << 32) | (uint64_t) ~(~(uint32_t) K[lane] & idm) : 0ull;
@@ -1619,6 +1734,11 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
     e = sort_keys_desc(w.sort_tmp, &bytes, w.keys, w.sorted, n, 32 + w.id_bits + rb, s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(TAIL_WG), 0, s, a, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_sum_replay(const double* t, int n, double acc0, int mode, double thr, double* out, hipStream_t s) {
+    hipLaunchKernelGGL(sum_replay_kernel, dim3(1), dim3(TAIL_WG), 0, s, t, n, acc0, mode, thr, out);
     return hipGetLastError();
 }
 

@@ -187,6 +187,17 @@ class Sampler:
         return ids[:n].copy(), pr[:n].copy(), int(nk.value), int(nkept.value)
 
 
+def debug_sum_replay(terms, acc0: float, mode: int = 0, thr: float = 0.0, stream=None):
+    """The wide tail's exact replay of acc = acc + terms[i] (device float64 tensor), in order; mode 1 stops at
+    acc >= thr, mode 2 at acc <= 0. Returns (result, stop index or -1)."""
+    import torch
+    out = torch.zeros(2, dtype=torch.float64, device=terms.device)
+    _lib.check(_lib.lib().kls_debug_sum_replay(_ptr(terms), int(terms.numel()), float(acc0), int(mode), float(thr),
+                                               _ptr(out), _stream_ptr(stream)), "kls_debug_sum_replay")
+    r = out.cpu().numpy()
+    return float(r[0]), int(r[1])
+
+
 def debug_expf(lo_bits: int, out, stream=None):
     """Device expf of float bit patterns lo_bits .. lo_bits+len(out)-1 into the torch float32 tensor `out`."""
     _lib.check(_lib.lib().kls_debug_expf(int(lo_bits), int(out.numel()), _ptr(out), _stream_ptr(stream)),
