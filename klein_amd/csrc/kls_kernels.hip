@@ -8,8 +8,8 @@
 //     of the segment's history ids staged in LDS; nothing is written to the logits or any global buffer;
 //   * greedy (sampler.cpp:31-39) keeps a per-lane (max, first id) and reduces across lanes and segments;
 //   * top-k (sampler.cpp:42-51): lanes contribute their largest logits (all 256 lanes of a 4-wave workgroup, the
-//     768 lanes of waves 0..11 of a 16-wave one); the k-th largest of those distinct logits is a lower bound of
-//     the segment's k-th largest value, and with the best bound
+//     lanes of waves 0..7 or 0..11 of a 16-wave one); the k-th largest of those distinct logits is a lower bound
+//     of the segment's k-th largest value, and with the best bound
 //     other workgroups of the row have published, one float compare per logit rejects nearly everything. The
 //     few survivors are ordered by a 64-bit key (value descending, id ascending) with wave64 bitonic networks
 //     built from DPP and permlane swaps;
