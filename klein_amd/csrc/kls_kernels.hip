@@ -8,8 +8,8 @@
 //     of the segment's history ids staged in LDS; nothing is written to the logits or any global buffer;
 //   * greedy (sampler.cpp:31-39) keeps a per-lane (max, first id) and reduces across lanes and segments;
 //   * top-k (sampler.cpp:42-51): lanes contribute their largest logits (all 256 lanes of a 4-wave workgroup, the
-//     lanes of waves 0..7 or 0..11 of a 16-wave one); the k-th largest of those distinct logits is a lower bound
-//     of the segment's k-th largest value, and with the best bound
+//     512 lanes of waves 0..7 of a 16-wave one); the k-th largest of those distinct logits is a lower bound of
+//     the segment's k-th largest value, and with the best bound
 //     other workgroups of the row have published, one float compare per logit rejects nearly everything. The
 //     few survivors are ordered by a 64-bit key (value descending, id ascending) with wave64 bitonic networks
 //     built from DPP and permlane swaps;
@@ -989,9 +989,9 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // (the barrier comes before the rest of the segment: every wave reaches it having issued few loads; a
         // wave whose loads wait for issue slots would hold the others here)
         __syncthreads();  // table zeroed
-        // Lazy 16-wave rows: waves 8..15, whose loads wait behind the first half's anyway, count before issuing
+        // Lazy 16-wave rows: waves 4..15, whose loads wait behind the first group's anyway, count before issuing
         // the middle batch, so that the table is complete (and the early bound can form) sooner.
-        const bool count_first = late && NW == 16 && wave >= 8;
+        const bool count_first = late && NW == 16 && wave >= 4;
         if (!count_first) load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
         if (!wide) {
             count_history<WG, C16, true>(a, row, lb, hi, hq, rh);
@@ -1117,15 +1117,14 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             for (int o = 1; o < NW; ++o) gl = merge32(gl, s_mx<NW>[o][63 - lane], lane);
         } else {
             // 16 waves: the early bound, from the lane maxima of the first eg groups of four waves alone (waves
-            // 0..7 or 0..11: 512 or 768 distinct logits of the segment, so still reached by k of them). Those waves
-            // receive their logits first (loads issue wave by wave), so the bound is usually ready when the later
-            // waves finish their scan, and they filter at once. Rows with penalties use three groups: lazily
-            // penalized lane maxima wait for the complete count table anyway, and the stronger bound passes fewer
-            // logits (measured: 8 waves are 0.6 µs faster without penalties, 0.8 µs slower with them). Each early wave
-            // sorts its lane maxima; the last of each group of four to arrive merges the group's lists, the last
-            // group to finish merges the groups' and publishes the k-th value. No wave waits before it has
-            // contributed, so every wait below ends.
-            constexpr int eg = PENALIZE ? 3 : 2;
+            // 0..7: 512 distinct logits of the segment, so still reached by k of them). Those waves receive their
+            // logits first (loads issue wave by wave), so the bound is usually ready when the later waves finish
+            // their scan, and they filter at once (measured on the 64-row batch: 0.75 µs less than with waves
+            // 0..11 without penalties, 0.25 µs less with them, where waves 4..15 count the history first). Each
+            // early wave sorts its lane maxima; the last of each group of four to arrive merges the group's lists,
+            // the last group to finish merges the groups' and publishes the k-th value. No wave waits before it
+            // has contributed, so every wait below ends.
+            constexpr int eg = 2;
             if (wave < 4 * eg) {
                 const int g = wave >> 2;
                 s_mx<NW>[wave][lane] = sort32<true>(ord_f32(m1), lane);
