@@ -944,7 +944,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // 16-wave top-k segments take their bound from waves 0..11 (the early bound, below); its LDS counters are
     // cleared before the barrier that follows the first batch (without penalties: one float4 per thread)
     constexpr bool EARLY = !GREEDY && NW == 16;
-    constexpr int Q1 = PENALIZE ? (NV >= 16 ? 4 : NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : EARLY ? 1 : NV;
+    constexpr int Q1 = PENALIZE ? (NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : EARLY ? 1 : NV;
     constexpr int Q3 = PENALIZE ? NV - NV / 4 : Q1;
     float v[EPT];
     RawHistory rh;
