@@ -941,7 +941,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // never held at once.
     const __amdgpu_buffer_rsrc_t seg_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(L + lb), (short) 0, SEG * 4, kRawBufferFlags);
-    // 16-wave top-k segments take their bound from waves 0..11 (the early bound, below); its LDS counters are
+    // 16-wave top-k segments take their bound from waves 0..7 (the early bound, below); its LDS counters are
     // cleared before the barrier that follows the first batch (without penalties: one float4 per thread)
     constexpr bool EARLY = !GREEDY && NW == 16;
     constexpr int Q1 = PENALIZE ? (NV >= 8 ? 2 : NV >= 2 ? 1 : 0) : EARLY ? 1 : NV;
@@ -1070,10 +1070,11 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             store_dev(&seg_out[0], m);
         }
     } else {
-        // ---- lower bound of the segment's k-th value: every lane contributes its largest and second largest
-        // logit (NaN counts as -inf and never reaches a bound); the k-th largest of these 2*WG distinct logits is
-        // reached by at least k logits of the segment. Each wave sorts its lane values and keeps its top 64,
-        // and the waves' lists are merged (in groups of four for 16 waves).
+        // ---- lower bound of the segment's k-th value: every lane contributes its largest logit (NaN counts as
+        // -inf and never reaches a bound); the k-th largest of these lane maxima (logits at distinct positions)
+        // is reached by at least k logits of the segment. Each wave sorts its lane maxima and keeps its top 64,
+        // and the waves' lists are merged (in groups of four for 16 waves). The second largest, m2, is kept for
+        // the filter, which skips a lane whose m2 falls below the bound (only its maximum can survive).
         // (canonicalized values: signaling NaNs quieted, so max ignores a NaN and med3 keeps m2, and every NaN fails
         // the filter's compares; med3(m1, m2, x) = max(m2, min(m1, x)) for m1 >= m2)
         float m1 = -INFINITY, m2 = -INFINITY;
