@@ -192,3 +192,25 @@ def test_verify_16_rows_penalized(torch_cuda, K, oracle_lib, wide):
         g.discard(acc + 1)
         accs.append(acc)
     S.close()
+
+
+@pytest.mark.parametrize("seg", (16384, 32768, 65536))
+def test_penalized_top_logits(torch_cuda, K, oracle_lib, seg):
+    """Penalties that can only lower logits (applied lazily) on 1024-thread segments, where the history holds a
+    row's largest raw logits: every lane maximum that forms the bound is a history id (row 0: the 2000 largest,
+    row 1: every other one of the 4000 largest, row 2: the 40 largest among Zipf ids), under heavy presence /
+    frequency or repetition penalties. Tokens and candidate lists bit-exact against the oracle."""
+    torch = torch_cuda
+    rng = np.random.default_rng(seg + 7)
+    V, rows = 248320, 3
+    x = head_rows(rng, rows, V)
+    order = np.argsort(-x, axis=1, kind="stable")
+    hists = [order[0, :2000].astype(np.int32),                                    # every top logit penalized
+             order[1, : 4000 : 2].astype(np.int32),                               # every other one
+             np.concatenate([order[2, :40], zipf_history(rng, V, 8000)]).astype(np.int32)]
+    for pp in (dict(presence_penalty=10.0, frequency_penalty=5.0, repetition_penalty=1.0),
+               dict(presence_penalty=0.5, frequency_penalty=0.2, repetition_penalty=4.0)):
+        for k in (64, 20, 1):
+            p = W.Params(temperature=1.0, top_k=k, top_p=0.9, **pp)
+            u = rng.random(rows)
+            check_batch(torch, K, oracle_lib, x, p, hists, u, seg, f"top penalized k{k} {pp}")
