@@ -231,12 +231,20 @@ def main():
     for i in range(a.warmup):
         step(i)
     torch.cuda.synchronize()
+    ts = [0] * (a.steps + 1)
+    pc = time.perf_counter_ns
     t0 = time.perf_counter()
+    ts[0] = pc()
     for i in range(a.steps):
         step(i)
+        ts[i + 1] = pc()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     us_step = (t1 - t0) / a.steps * 1e6
+    per = [(ts[i + 1] - ts[i]) / 1e3 for i in range(a.steps)]
+    srt = sorted(per)
+    lat = {"first_25_us": [round(x, 1) for x in per[:25]], "median_us": round(srt[len(srt) // 2], 2),
+           "p99_us": round(srt[min(len(srt) - 1, (len(srt) * 99) // 100)], 2)}
 
     # kernel device time per launch: the same fused kernel over the same 4 rows, launched back to back on the
     # stream (device-resident uniforms, no host round trip between launches), one event pair around n launches
@@ -275,7 +283,7 @@ def main():
            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
            "config": {"workload": "mtp_verify_step", "rows": 4, "vocab": V, "drafts": 3, "temperature": 0.6,
                       "top_k": 20, "top_p": 0.95, "hipgraph": True, "logits": "resident in HBM"},
-           "roofline": roof}
+           "latency": lat, "roofline": roof}
 
     # ---------------- 64-row batched stress
     if not a.no_batched:

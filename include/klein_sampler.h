@@ -45,7 +45,8 @@ typedef struct kls_params {
 
 typedef struct kls_sampler* kls_handle;
 
-/* hipStream_t, passed as a plain pointer; NULL selects the handle's own stream. */
+/* hipStream_t, passed as a plain pointer; NULL selects the library's own stream of the handle's device (one per
+ * device, shared by every handle created on it). */
 typedef void* kls_stream;
 
 /* Replaces Sampler::Sampler (src/sampler.cpp:11). Binds the current HIP device, allocates every buffer the
@@ -60,7 +61,11 @@ int kls_destroy(kls_handle h);
 /* Replaces Sampler::reset (src/sampler.cpp:13): clears the token history. */
 int kls_reset(kls_handle h);
 
-/* Replaces Sampler::accept (src/sampler.cpp:15): counts one more occurrence of `token` for the penalties. */
+/* Replaces Sampler::accept (src/sampler.cpp:15): counts one more occurrence of `token` for the penalties.
+ * Calls that use the handle (this one included) are refused with KLS_ERR_INVALID_ARG while a verify step is in
+ * flight (between kls_verify_enqueue and kls_verify_wait). The asynchronous calls that lend the handle's scratch
+ * (kls_sample_batch, kls_argmax, kls_ppl_scores) are ordered after the handle's earlier launches when they come
+ * on another stream. */
 int kls_accept(kls_handle h, int32_t token);
 
 /* Replaces Sampler::sample (src/sampler.cpp:17-89) for one row of n_vocab f32 logits. `logits` may be a device
@@ -75,7 +80,11 @@ int kls_sample(kls_handle h, const float* logits, int n_vocab, double u, int32_t
  * On return out_tokens[0..*out_accepted] are the emitted tokens (later entries are unspecified) and the
  * emitted tokens have been added to the history, as the engine's accept(t) calls do (engine.cpp:567).
  * The caller-side stops of the engine (end-of-generation token, n_predict, callback) stay with the caller.
- * The step runs as one hipGraph launch on `stream`; host-side inputs and outputs go through pinned memory. */
+ * The step runs as one hipGraph launch on `stream`; host-side inputs and outputs go through pinned memory. The
+ * accepted count is formed on the device, by the workgroup that completes the last row, and also stays in
+ * device memory with the tokens (kls_device_results) for work that follows on the stream. The first verify
+ * step on a stream first runs a short series of empty graph launches through it (once per stream and process:
+ * this ROCm's first graph launches on a stream cost several times the later ones). */
 int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
                int32_t* out_tokens, int32_t* out_accepted, kls_stream stream);
 
@@ -86,6 +95,19 @@ int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts,
 int kls_verify_enqueue(kls_handle h, const float* logits, int nb, const int32_t* drafts, const double* u,
                        kls_stream stream);
 int kls_verify_wait(kls_handle h, int32_t* out_tokens, int32_t* out_accepted);
+
+/* No counterpart in the reference (whose results live on the host): the device buffers that hold the last
+ * verify step's results, for consumers enqueued after it on the same stream: d_tokens[i] is row i's token
+ * (i < nb), *d_accepted the accepted count. Valid for the handle's lifetime; overwritten by the next step
+ * (kls_sample and kls_sample_batch without an output of their own write d_tokens too). Either pointer may be
+ * NULL. */
+int kls_device_results(kls_handle h, const int32_t** d_tokens, const int32_t** d_accepted);
+
+/* No counterpart in the reference: reports (once) KLS_ERR_HIP if a kernel launched for this handle gave up an
+ * internal wait since the last check, in which case that call's results are not valid. The synchronous calls
+ * (kls_sample, kls_verify, kls_verify_wait) check by themselves after their step; callers of the asynchronous
+ * ones check after synchronizing the stream (every call also checks on entry). */
+int kls_check(kls_handle h);
 
 /* Batched sampling of n_rows independent rows, all on the device, asynchronous on `stream` (no host sync).
  * Row r is at d_logits + r*row_stride floats; its token history is d_hist_ids[d_hist_off[r] .. d_hist_off[r+1])
@@ -128,6 +150,23 @@ int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int ca
  * patterns lo, lo+1, ... to device memory `d_out`, asynchronously on `stream`, so tests can compare the device
  * exponential with the host libm's std::exp(float) (src/sampler.cpp:57) over whole ranges of inputs. */
 int kls_debug_expf(uint32_t lo, long long n, float* d_out, kls_stream stream);
+
+/* Test hook, no counterpart in the reference: overrides the launch layout the handle chooses (a field of 0 keeps
+ * the default; xcd_map -1 keeps it): seg_len = vocabulary ids per workgroup (a power of two in [1024, 65536]),
+ * target_wg / wide_target_wg = the grid sizes the segment choice aims at, share_min_wg = the grid size above
+ * which workgroups of a row share a running bound through device memory, xcd_map = 1 to deal a row's segments
+ * to one XCD, 0 for plain order. Results do not depend on the layout; tests use it to reach every code path.
+ * wait_limit bounds the polls of the kernels' internal waits (0: the default, 2^20; negative: none, so such a
+ * wait gives up at once and the call reports KLS_ERR_HIP): tests force the failure path with it. */
+typedef struct kls_debug_layout {
+    int32_t seg_len;
+    int32_t target_wg;
+    int32_t wide_target_wg;
+    int32_t share_min_wg;
+    int32_t xcd_map;
+    int32_t wait_limit;
+} kls_debug_layout;
+int kls_debug_set_layout(kls_handle h, const kls_debug_layout* layout);
 
 /* Test hook, no counterpart in the reference: the wide top-k tail's parallel replay of a sequential double sum
  * (src/sampler.cpp:58,70-77,84-87 accumulate this way) over the n device doubles d_terms from acc0:

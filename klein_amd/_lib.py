@@ -20,13 +20,19 @@ KLS_ERR_OOM = 6
 # every entry point include/klein_sampler.h declares
 EXPORTS = ["kls_create", "kls_destroy", "kls_reset", "kls_accept", "kls_sample", "kls_verify", "kls_verify_enqueue",
            "kls_verify_wait", "kls_sample_batch", "kls_argmax", "kls_ppl_scores",
-           "kls_get_candidates", "kls_debug_expf", "kls_debug_sum_replay", "kls_status_string", "kls_last_error"]
+           "kls_device_results", "kls_check", "kls_get_candidates", "kls_debug_set_layout", "kls_debug_expf",
+           "kls_debug_sum_replay", "kls_status_string", "kls_last_error"]
 
 
 class KlsParams(C.Structure):
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("min_p", C.c_float),
                 ("presence_penalty", C.c_float), ("frequency_penalty", C.c_float),
                 ("repetition_penalty", C.c_float), ("seed", C.c_uint64)]
+
+
+class KlsDebugLayout(C.Structure):
+    _fields_ = [("seg_len", C.c_int32), ("target_wg", C.c_int32), ("wide_target_wg", C.c_int32),
+                ("share_min_wg", C.c_int32), ("xcd_map", C.c_int32), ("wait_limit", C.c_int32)]
 
 
 class KlsError(RuntimeError):
@@ -61,6 +67,9 @@ def lib():
                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                      C.c_void_p]
         L.kls_get_candidates.argtypes = [P, C.c_int, I32P, F32P, C.c_int, I32P, I32P]
+        L.kls_device_results.argtypes = [P, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]
+        L.kls_check.argtypes = [P]
+        L.kls_debug_set_layout.argtypes = [P, C.POINTER(KlsDebugLayout)]
         L.kls_debug_expf.argtypes = [C.c_uint32, C.c_longlong, C.c_void_p, C.c_void_p]
         L.kls_debug_sum_replay.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_int, C.c_double, C.c_void_p,
                                            C.c_void_p]

@@ -12,8 +12,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "klein_sampler.h"
@@ -50,8 +52,15 @@ struct kls_sampler {
     int k = 0;
     int V = 0, max_rows = 0, device = 0;
     int bucket_shift = MIN_BUCKET_SHIFT, n_buckets = 0;
+    // launch layout (defaults; kls_debug_set_layout overrides them for tests)
     int seg_len_override = 0, target_wg = 128, wide_target_wg = 320, share_min_wg = 1024, xcd_map = 1;
-    hipStream_t stream = nullptr;
+    int spin_limit = DEFAULT_SPIN_LIMIT;
+    hipStream_t stream = nullptr;  // the library's stream of this device (shared by handles; not destroyed)
+    // ordering of launches that share the scratch: the stream of the last launch, and an event that makes a
+    // launch on another stream wait for it
+    hipStream_t last_stream = nullptr;
+    hipEvent_t order_ev = nullptr;
+    const void* dev_ptr = nullptr;  // the last logits pointer found to be device memory
 
     // token history: host copy (as the reference's counts_) + what has reached the device
     std::unordered_map<int32_t, int32_t> counts;
@@ -67,6 +76,8 @@ struct kls_sampler {
     uint32_t* d_row_ticket = nullptr;
     uint64_t* d_row_thr = nullptr;
     int32_t* d_tokens = nullptr;
+    int32_t* d_accepted = nullptr;  // accepted count of the last verify step
+    uint64_t* d_step = nullptr;     // the verify step's row counter and mismatch bits (left zero)
     uint64_t* d_dbg_keys = nullptr;
     float* d_dbg_probs = nullptr;
     int32_t* d_dbg_meta = nullptr;
@@ -91,8 +102,11 @@ struct kls_sampler {
     bool inflight = false;
     hipStream_t inflight_stream = nullptr;
     int inflight_rows = 0;
+    bool inflight_verify = false;
+    int32_t accepted = 0;  // accepted count of the last completed verify step (as the device formed it)
     const float* g_logits = nullptr;
     int g_rows = 0;
+    bool g_count_wide = false;
     bool g_valid = false;
 };
 
@@ -106,6 +120,77 @@ bool is_device_ptr(const void* p) {
         return false;
     }
     return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+// The engine passes the same logits buffer every step: the last pointer found to be device memory is
+// remembered, so a step makes no pointer query.
+bool is_device_logits(kls_sampler* h, const void* p) {
+    if (p == h->dev_ptr) return true;
+    if (!is_device_ptr(p)) return false;
+    h->dev_ptr = p;
+    return true;
+}
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_mu;                                 // guards everything below
+hipStream_t g_stream[MAX_DEVICES] = {};          // the library's stream per device
+hipGraphExec_t g_prep_exec[MAX_DEVICES] = {};    // a graph of one empty kernel per device
+std::unordered_set<hipStream_t> g_graph_ready;   // streams that have carried PREP_LAUNCHES graph launches
+
+// The library's own stream of `device` (created on first use, kept for the process): handles created without
+// a caller stream share it, so a new handle costs no stream creation and starts on a stream that is ready for
+// graph launches.
+hipError_t library_stream(int device, hipStream_t* out) {
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_stream[device]) {
+        const hipError_t e = hipStreamCreateWithFlags(&g_stream[device], hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            g_stream[device] = nullptr;
+            return e;
+        }
+    }
+    *out = g_stream[device];
+    return hipSuccess;
+}
+
+// On this ROCm the first few dozen graph launches on a stream cost two to three times the host time of later
+// ones (measured on MI355X with a one-kernel graph: ~40 us instead of ~16 us for the first 40 launches of a new
+// stream; launches of another graph on the stream beforehand remove the difference, direct kernel launches and
+// hipGraphUpload do not). Before the first verify step on a stream, PREP_LAUNCHES launches of a graph of one
+// empty kernel go through it (~3 ms, once per stream and process).
+constexpr int PREP_LAUNCHES = 128;
+
+hipError_t prepare_graph_stream(int device, hipStream_t s) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_graph_ready.count(s)) return hipSuccess;
+    hipError_t e;
+    if (!g_prep_exec[device]) {
+        hipGraph_t g = nullptr;
+        if ((e = hipGraphCreate(&g, 0)) != hipSuccess) return e;
+        int unused = 0;
+        void* args[] = {&unused};
+        hipKernelNodeParams np{};
+        np.func = const_cast<void*>(noop_kernel());
+        np.gridDim = dim3(1);
+        np.blockDim = dim3(64);
+        np.sharedMemBytes = 0;
+        np.kernelParams = args;
+        np.extra = nullptr;
+        hipGraphNode_t node;
+        e = hipGraphAddKernelNode(&node, g, nullptr, 0, &np);
+        if (e == hipSuccess) e = hipGraphInstantiate(&g_prep_exec[device], g, nullptr, nullptr, 0);
+        (void) hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            g_prep_exec[device] = nullptr;
+            return e;
+        }
+    }
+    for (int i = 0; i < PREP_LAUNCHES; ++i)
+        if ((e = hipGraphLaunch(g_prep_exec[device], s)) != hipSuccess) return e;
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+    g_graph_ready.insert(s);
+    return hipSuccess;
 }
 
 // Segment length. First choice, for vocabularies of at least 16384 ids: 1024-thread workgroups over
@@ -166,8 +251,10 @@ int upload_history(kls_sampler* h, hipStream_t s) {
     KLS_HIP(hipMemcpyAsync(h->d_hist_boff, bo, sizeof(int32_t) * (h->n_buckets + 1), hipMemcpyHostToDevice, s));
     KLS_HIP(hipStreamSynchronize(s));
     h->pending.clear();
-    // counts on the device add at most the pending ids and a step's drafts to the uploaded ones
+    // counts on the device add at most the pending ids and a step's drafts to the uploaded ones; the captured
+    // verify graph bakes the table width in, so a change of width invalidates it
     h->count_wide = (int64_t) max_count + PENDING_CAP + VERIFY_MAX_ROWS >= 65536;
+    if (h->count_wide != h->g_count_wide) h->g_valid = false;
     return KLS_OK;
 }
 
@@ -190,6 +277,8 @@ RowsArgs base_args(kls_sampler* h, const float* logits, int rows, int64_t stride
     a.dbg_keys = h->d_dbg_keys;
     a.dbg_probs = h->d_dbg_probs;
     a.dbg_meta = h->d_dbg_meta;
+    a.fault = &h->res_dev->fault;
+    a.spin_limit = h->spin_limit;
     return a;
 }
 
@@ -211,12 +300,45 @@ RowsArgs step_args(kls_sampler* h, const float* logits, int rows, bool verify) {
     a.u = h->call_dev->u;
     a.host_res = h->res_dev;
     a.call = h->call_dev;
+    if (verify) {
+        a.step_word = h->d_step;
+        a.out_accepted = h->d_accepted;
+    }
     return a;
 }
 
 int check_handle(kls_handle h) {
     if (!h) return fail(KLS_ERR_INVALID_ARG, "null handle");
     return KLS_OK;
+}
+
+// Turns a fault a kernel of this handle reported (an internal wait that gave up) into an error, once.
+int check_fault(kls_sampler* h) {
+    const uint32_t f = __atomic_load_n(&h->res->fault, __ATOMIC_ACQUIRE);
+    if (f == 0u) return KLS_OK;
+    __atomic_store_n(&h->res->fault, 0u, __ATOMIC_RELEASE);
+    char buf[160];
+    snprintf(buf, sizeof buf, "a sampling kernel of this handle gave up an internal wait (code %u): its results are "
+                              "not valid", f);
+    return fail(KLS_ERR_HIP, buf);
+}
+
+// Orders a launch on `s` after the handle's previous launches, which share its scratch: when the stream changes,
+// `s` waits for everything enqueued on the previous one so far.
+int order_on(kls_sampler* h, hipStream_t s) {
+    if (h->last_stream && h->last_stream != s) {
+        KLS_HIP(hipEventRecord(h->order_ev, h->last_stream));
+        KLS_HIP(hipStreamWaitEvent(s, h->order_ev, 0));
+    }
+    h->last_stream = s;
+    return KLS_OK;
+}
+
+// Entry checks of the asynchronous calls that lend the handle's scratch.
+int check_async(kls_sampler* h, hipStream_t s) {
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a verify or sample step is in flight on this handle");
+    if (int st = check_fault(h)) return st;
+    return order_on(h, s);
 }
 
 // Brings the device history up to date before a step: pending ids ride in the call block up to its capacity.
@@ -231,11 +353,13 @@ int prepare_history(kls_sampler* h, hipStream_t s) {
     return KLS_OK;
 }
 
-// Enqueues one step over `rows` rows of the handle's history on `s`; results land in the pinned block.
+// Enqueues one step over `rows` rows of the handle's history on `s`; results land in the pinned block. The
+// caller has checked that no step is in flight and written the step's uniforms (and drafts) to the call block.
 int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hipStream_t s) {
-    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is already in flight on this handle");
+    if (int st = check_fault(h)) return st;
+    if (int st = order_on(h, s)) return st;
     const float* dl = logits;
-    if (!is_device_ptr(logits)) {
+    if (!is_device_logits(h, logits)) {
         KLS_HIP(hipMemcpyAsync(h->d_rows_buf, logits, sizeof(float) * (size_t) rows * h->V, hipMemcpyHostToDevice, s));
         dl = h->d_rows_buf;
     }
@@ -254,18 +378,24 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
             h->gexec = nullptr;
             h->graph = nullptr;
             h->g_valid = false;
-            KLS_HIP(hipStreamBeginCapture(h->stream, hipStreamCaptureModeRelaxed));
-            const hipError_t le = launch_rows(a, h->greedy, h->penalize, h->stream);
+            hipStream_t cap = nullptr;
+            KLS_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+            const hipError_t be = hipStreamBeginCapture(cap, hipStreamCaptureModeRelaxed);
+            const hipError_t le = be == hipSuccess ? launch_rows(a, h->greedy, h->penalize, cap) : hipSuccess;
             hipGraph_t g = nullptr;
-            const hipError_t ce = hipStreamEndCapture(h->stream, &g);
+            const hipError_t ce = be == hipSuccess ? hipStreamEndCapture(cap, &g) : hipSuccess;
+            (void) hipStreamDestroy(cap);
+            if (be != hipSuccess) return fail(KLS_ERR_HIP, "hipStreamBeginCapture", be);
             if (le != hipSuccess) return fail(KLS_ERR_HIP, "launch_rows (capture)", le);
             if (ce != hipSuccess) return fail(KLS_ERR_HIP, "hipStreamEndCapture", ce);
             h->graph = g;
             KLS_HIP(hipGraphInstantiate(&h->gexec, h->graph, nullptr, nullptr, 0));
             h->g_logits = dl;
             h->g_rows = rows;
+            h->g_count_wide = h->count_wide;
             h->g_valid = true;
         }
+        KLS_HIP(prepare_graph_stream(h->device, s));
         KLS_HIP(hipGraphLaunch(h->gexec, s));
     } else {
         KLS_HIP(launch_rows(a, h->greedy, h->penalize, s));
@@ -273,17 +403,25 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
     h->inflight = true;
     h->inflight_stream = s;
     h->inflight_rows = rows;
+    h->inflight_verify = verify;
     return KLS_OK;
 }
 
-// Waits for the in-flight step: spins on the per-row sequence numbers the kernel publishes after each row's
-// token, falling back to a stream synchronization after 50 ms (queued work ahead of the step, or a failure).
+// Waits for the in-flight step: spins on the sequence numbers the kernel publishes (a verify step's accepted
+// count, then each row's token), falling back to a stream synchronization after 50 ms (queued work ahead of the
+// step, or a failure).
 int wait_step(kls_sampler* h) {
     if (!h->inflight) return fail(KLS_ERR_INVALID_ARG, "no step in flight on this handle");
     h->inflight = false;
     const uint32_t want = h->call->seq;
     const int rows = h->inflight_rows;
+    const bool verify = h->inflight_verify;
     auto done = [&] {
+        if (verify) {
+            const uint64_t w = __atomic_load_n(&h->res->step_word, __ATOMIC_ACQUIRE);
+            if ((uint32_t) (w >> 32) != want) return false;
+            h->accepted = (int32_t) (uint32_t) w;
+        }
         for (int r = 0; r < rows; ++r) {
             const uint64_t w = __atomic_load_n(&h->res->row_word[r], __ATOMIC_ACQUIRE);
             if ((uint32_t) (w >> 32) != want) return false;
@@ -295,19 +433,23 @@ int wait_step(kls_sampler* h) {
     while (!done()) {
         if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(50)) {
             KLS_HIP(hipStreamSynchronize(h->inflight_stream));
-            if (!done()) return fail(KLS_ERR_HIP, "step result not published");
+            if (!done()) {
+                if (int st = check_fault(h)) return st;
+                return fail(KLS_ERR_HIP, "step result not published");
+            }
             break;
         }
 #if defined(__x86_64__)
         __builtin_ia32_pause();
 #endif
     }
-    return KLS_OK;
+    return check_fault(h);
 }
 
 void add_history(kls_sampler* h, int32_t t) {
     h->counts[t]++;
-    h->pending.push_back(t);
+    // (the device copy of the history is read only with penalties)
+    if (h->penalize) h->pending.push_back(t);
 }
 
 }  // namespace
@@ -332,19 +474,20 @@ const char* kls_last_error(void) { return g_err.c_str(); }
 int kls_destroy(kls_handle h) {
     if (!h) return fail(KLS_ERR_INVALID_ARG, "null handle");
     (void) hipSetDevice(h->device);
-    if (h->stream) (void) hipStreamSynchronize(h->stream);
+    // (the handle's work may be on any stream it was given: wait for the device)
+    (void) hipDeviceSynchronize();
     if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
     if (h->graph) (void) hipGraphDestroy(h->graph);
     void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_seg_cand,
-                   h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_dbg_keys,
-                   h->d_dbg_probs, h->d_dbg_meta, h->d_rows_buf, h->w.keys,
-                   h->w.sorted, h->w.sort_tmp};
+                   h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_accepted,
+                   h->d_step, h->d_dbg_keys, h->d_dbg_probs, h->d_dbg_meta,
+                   h->d_rows_buf, h->w.keys, h->w.sorted, h->w.sort_tmp};
     for (void* p : dev)
         if (p) (void) hipFree(p);
     if (h->h_stage) (void) hipHostFree(h->h_stage);
     if (h->call) (void) hipHostFree(h->call);
     if (h->res) (void) hipHostFree(h->res);
-    if (h->stream) (void) hipStreamDestroy(h->stream);
+    if (h->order_ev) (void) hipEventDestroy(h->order_ev);
     delete h;
     return KLS_OK;
 }
@@ -382,11 +525,6 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
                             params->frequency_penalty >= 0.0f) ? 1 : 0};
     while (((n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift) > MAX_BUCKETS) h->bucket_shift++;
     h->n_buckets = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;
-    if (const char* e = getenv("KLS_SEG_LEN")) h->seg_len_override = atoi(e);
-    if (const char* e = getenv("KLS_TARGET_WG")) h->target_wg = std::max(1, atoi(e));
-    if (const char* e = getenv("KLS_WIDE_TARGET_WG")) h->wide_target_wg = std::max(1, atoi(e));
-    if (const char* e = getenv("KLS_SHARE_MIN_WG")) h->share_min_wg = atoi(e);
-    if (const char* e = getenv("KLS_XCD_MAP")) h->xcd_map = atoi(e) != 0;
     (void) hipGetDevice(&h->device);
 
     auto oom = [&](const char* what, hipError_t e) {
@@ -394,7 +532,11 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
         return fail(KLS_ERR_OOM, what, e);
     };
     hipError_t e;
-    if ((e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking)) != hipSuccess) return oom("stream", e);
+    if ((e = library_stream(h->device, &h->stream)) != hipSuccess) {
+        kls_destroy(h);
+        return fail(KLS_ERR_HIP, "library stream", e);
+    }
+    if ((e = hipEventCreateWithFlags(&h->order_ev, hipEventDisableTiming)) != hipSuccess) return oom("event", e);
     if ((e = prepare_rows_kernels()) != hipSuccess) {
         kls_destroy(h);
         return fail(KLS_ERR_HIP, "kernel LDS limits", e);
@@ -410,6 +552,8 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     ALLOC(h->d_row_ticket, sizeof(uint32_t) * R);
     ALLOC(h->d_row_thr, sizeof(uint64_t) * R);
     ALLOC(h->d_tokens, sizeof(int32_t) * R);
+    ALLOC(h->d_accepted, sizeof(int32_t));
+    ALLOC(h->d_step, sizeof(uint64_t));
     ALLOC(h->d_dbg_keys, sizeof(uint64_t) * R * KCAP);
     ALLOC(h->d_dbg_probs, sizeof(float) * R * KCAP);
     ALLOC(h->d_dbg_meta, sizeof(int32_t) * R * 2);
@@ -443,6 +587,8 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     if ((e = hipMemsetAsync(h->d_row_thr, 0, sizeof(uint64_t) * R, h->stream)) != hipSuccess) return oom("init", e);
     if ((e = hipMemsetAsync(h->d_hist_boff, 0, sizeof(int32_t) * (h->n_buckets + 1), h->stream)) != hipSuccess)
         return oom("init", e);
+    if ((e = hipMemsetAsync(h->d_step, 0, sizeof(uint64_t), h->stream)) != hipSuccess) return oom("init", e);
+    if ((e = hipMemsetAsync(h->d_accepted, 0, sizeof(int32_t), h->stream)) != hipSuccess) return oom("init", e);
     if ((e = hipStreamSynchronize(h->stream)) != hipSuccess) return oom("init", e);
     *out = h;
     return KLS_OK;
@@ -450,6 +596,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
 
 int kls_reset(kls_handle h) {
     if (int st = check_handle(h)) return st;
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is in flight on this handle");
     h->counts.clear();
     h->pending.clear();
     (void) hipSetDevice(h->device);
@@ -459,6 +606,7 @@ int kls_reset(kls_handle h) {
 int kls_accept(kls_handle h, int32_t token) {
     if (int st = check_handle(h)) return st;
     if (token < 0 || token >= h->V) return fail(KLS_ERR_RANGE, "token outside [0, n_vocab)");
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is in flight on this handle");
     add_history(h, token);
     return KLS_OK;
 }
@@ -467,6 +615,8 @@ int kls_sample(kls_handle h, const float* logits, int n_vocab, double u, int32_t
     if (int st = check_handle(h)) return st;
     if (!logits || !out_token) return fail(KLS_ERR_INVALID_ARG, "null argument");
     if (n_vocab != h->V) return fail(KLS_ERR_INVALID_ARG, "n_vocab differs from the handle's");
+    // (checked before the call block is written: a running step reads it)
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is already in flight on this handle");
     (void) hipSetDevice(h->device);
     h->call->u[0] = u;
     int st = enqueue_step(h, logits, 1, false, h->stream);
@@ -482,6 +632,8 @@ int kls_verify_enqueue(kls_handle h, const float* logits, int nb, const int32_t*
     if (!logits || !u || (nb > 1 && !drafts)) return fail(KLS_ERR_INVALID_ARG, "null argument");
     if (nb < 1) return fail(KLS_ERR_INVALID_ARG, "nb must be at least 1");
     if (nb > h->max_rows || nb > VERIFY_MAX_ROWS) return fail(KLS_ERR_RANGE, "nb above the handle's capacity");
+    // (checked before the call block is written: a running step reads it)
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is already in flight on this handle");
     (void) hipSetDevice(h->device);
     hipStream_t s = stream ? (hipStream_t) stream : h->stream;
     for (int i = 0; i < nb; ++i) h->call->u[i] = u[i];
@@ -492,16 +644,14 @@ int kls_verify_enqueue(kls_handle h, const float* logits, int nb, const int32_t*
 int kls_verify_wait(kls_handle h, int32_t* out_tokens, int32_t* out_accepted) {
     if (int st = check_handle(h)) return st;
     if (!out_tokens || !out_accepted) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (h->inflight && !h->inflight_verify) return fail(KLS_ERR_INVALID_ARG, "no verify step in flight on this handle");
     const int nb = h->inflight_rows;
     if (int st = wait_step(h)) return st;
-    // engine.cpp:571-573: draft i+1 is accepted while it equals the token sampled at position i
-    int acc = 0;
-    while (acc < nb - 1 && h->tokens[acc] == h->call->drafts[acc]) ++acc;
-    for (int i = 0; i <= acc; ++i) {
-        out_tokens[i] = h->tokens[i];
-        add_history(h, out_tokens[i]);
-    }
-    for (int i = acc + 1; i < nb; ++i) out_tokens[i] = h->tokens[i];
+    // the accepted count as the device formed it (engine.cpp:564-575: drafts accepted while batch[i+1] == t_i)
+    const int acc = h->accepted;
+    if (acc < 0 || acc >= nb) return fail(KLS_ERR_HIP, "accepted count out of range");
+    for (int i = 0; i < nb; ++i) out_tokens[i] = h->tokens[i];
+    for (int i = 0; i <= acc; ++i) add_history(h, out_tokens[i]);
     *out_accepted = acc;
     return KLS_OK;
 }
@@ -512,6 +662,38 @@ int kls_verify(kls_handle h, const float* logits, int nb, const int32_t* drafts,
     if (!out_tokens || !out_accepted) return fail(KLS_ERR_INVALID_ARG, "null argument");
     if (int st = kls_verify_enqueue(h, logits, nb, drafts, u, stream)) return st;
     return kls_verify_wait(h, out_tokens, out_accepted);
+}
+
+int kls_device_results(kls_handle h, const int32_t** d_tokens, const int32_t** d_accepted) {
+    if (int st = check_handle(h)) return st;
+    if (!d_tokens && !d_accepted) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (d_tokens) *d_tokens = h->d_tokens;
+    if (d_accepted) *d_accepted = h->d_accepted;
+    return KLS_OK;
+}
+
+int kls_check(kls_handle h) {
+    if (int st = check_handle(h)) return st;
+    return check_fault(h);
+}
+
+int kls_debug_set_layout(kls_handle h, const kls_debug_layout* l) {
+    if (int st = check_handle(h)) return st;
+    if (!l) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is in flight on this handle");
+    const int o = l->seg_len;
+    if (o != 0 && (o < SEG_MIN || o > SEG_MAX || (o & (o - 1)) != 0))
+        return fail(KLS_ERR_INVALID_ARG, "segment length must be 0 or a power of two in [1024, 65536]");
+    if (l->target_wg < 0 || l->wide_target_wg < 0 || l->share_min_wg < 0 || l->xcd_map < -1 || l->xcd_map > 1)
+        return fail(KLS_ERR_INVALID_ARG, "layout field out of range");
+    h->seg_len_override = o;
+    if (l->target_wg) h->target_wg = l->target_wg;
+    if (l->wide_target_wg) h->wide_target_wg = l->wide_target_wg;
+    if (l->share_min_wg) h->share_min_wg = l->share_min_wg;
+    if (l->xcd_map >= 0) h->xcd_map = l->xcd_map;
+    h->spin_limit = l->wait_limit == 0 ? DEFAULT_SPIN_LIMIT : l->wait_limit < 0 ? 0 : l->wait_limit;
+    h->g_valid = false;  // (the verify graph bakes the layout in)
+    return KLS_OK;
 }
 
 int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_hist_off,
@@ -525,6 +707,7 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
     if (row_stride < h->V) return fail(KLS_ERR_INVALID_ARG, "row_stride below n_vocab");
     (void) hipSetDevice(h->device);
     hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    if (int st = check_async(h, s)) return st;
     RowsArgs a = base_args(h, d_logits, n_rows, row_stride, h->greedy);
     const bool pen = h->penalize && d_hist_off != nullptr;
     if (pen) {
@@ -549,6 +732,7 @@ int kls_argmax(kls_handle h, const float* d_logits, int n_rows, int64_t row_stri
     if (row_stride < h->V) return fail(KLS_ERR_INVALID_ARG, "row_stride below n_vocab");
     (void) hipSetDevice(h->device);
     hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    if (int st = check_async(h, s)) return st;
     RowsArgs a = base_args(h, d_logits, n_rows, row_stride, true);
     a.out_tokens = d_out;
     a.first_nan = 1;
@@ -570,6 +754,7 @@ int kls_ppl_scores(kls_handle h, const float* d_logits, int n_rows, int64_t row_
     if (row_stride < h->V || (d_base && base_stride < h->V)) return fail(KLS_ERR_INVALID_ARG, "row stride below n_vocab");
     (void) hipSetDevice(h->device);
     hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    if (int st = check_async(h, s)) return st;
     PplArgs a{};
     a.logits = d_logits;
     a.row_stride = row_stride;
@@ -596,6 +781,7 @@ int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int ca
     if (int st = check_handle(h)) return st;
     if (row < 0 || row >= h->max_rows) return fail(KLS_ERR_RANGE, "row outside the handle's capacity");
     if (cap < 0 || (cap > 0 && (!ids || !probs))) return fail(KLS_ERR_INVALID_ARG, "bad output buffers");
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is in flight on this handle");
     (void) hipSetDevice(h->device);
     KLS_HIP(hipDeviceSynchronize());
     uint64_t keys[KCAP];

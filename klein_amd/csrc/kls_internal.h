@@ -32,10 +32,19 @@ struct CallBlock {
 };
 
 // Results a step writes back to pinned host memory: per row one 64-bit word, (sequence number << 32) | token,
-// stored at once so the host sees either the old word or the new one.
+// stored at once so the host sees either the old word or the new one; for a verify step one more word,
+// (sequence number << 32) | accepted, written by the workgroup that completes the step's last row.
 struct ResultBlock {
     uint64_t row_word[VERIFY_MAX_ROWS];
+    uint64_t step_word;
+    // nonzero: a kernel launched for this handle found an internal wait that did not end (the code names it);
+    // set by the device, read and cleared by the host
+    uint32_t fault;
 };
+
+// Fault codes (ResultBlock::fault).
+constexpr uint32_t FAULT_COUNT_WAIT = 1;   // the history count table was not announced complete in time
+constexpr uint32_t FAULT_BOUND_WAIT = 2;   // the early bound of a 16-wave segment was not published in time
 
 struct SamplingParams {
     float temperature;
@@ -94,8 +103,18 @@ struct RowsArgs {
     float* dbg_probs;       // [n_rows][KCAP]
     int32_t* dbg_meta;      // [n_rows][2]: k, kept
     ResultBlock* host_res;  // pinned, may be NULL: tokens and per-row sequence numbers for the host
-    const CallBlock* call;  // the sequence number to publish (with host_res)
+    const CallBlock* call;  // the sequence number to publish (with host_res), the drafts of a verify step
+    // verify steps (src/engine.cpp:563-575): the accept prefix on the device. Each row's last workgroup adds
+    // (1 << 32) | (mismatch of row r: 1 << r) to *step_word; the one that completes the count forms
+    // accepted = the first row whose token differs from its draft (the last row if none), writes it to
+    // *out_accepted and to host_res->step_word, and clears *step_word for the next launch. NULL: no accept.
+    uint64_t* step_word;
+    int32_t* out_accepted;
+    uint32_t* fault;        // mapped pinned word, may be NULL: set when an internal wait gives up
+    int32_t spin_limit;     // polls of an internal wait before it gives up (a guard: the waits always end)
 };
+
+constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 20;
 
 
 // Wide top-k (k above KCAP, up to no limit; src/sampler.cpp:42-51): every logit of a row becomes one 64-bit key
@@ -142,6 +161,8 @@ hipError_t launch_rows(const RowsArgs& a, bool greedy, bool penalize, hipStream_
 int rows_grid(const RowsArgs& a);  // workgroups launch_rows starts
 hipError_t prepare_rows_kernels();  // once per device: LDS limits of the kernels with large count tables
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s);
+// A kernel that does nothing (one wave): the body of the graph that prepares a stream for graph launches.
+const void* noop_kernel();
 // Test hook of the wide tail's exact sum replay (see kls_debug_sum_replay).
 hipError_t launch_sum_replay(const double* t, int n, double acc0, int mode, double thr, double* out, hipStream_t s);
 // Wide top-k: keys (with penalties from the history in `a`), the sort, the tail (tokens published as

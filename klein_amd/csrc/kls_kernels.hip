@@ -16,7 +16,9 @@
 //   * the last workgroup of a row (ticket counter) merges the segment candidate lists into the row's sorted
 //     top-k and runs the O(k) tail on one wave: softmax with temperature (expf bit-identical to the host
 //     glibc's, double sums), min-p, top-p and the draw (sampler.cpp:53-88);
-//   * in a verify step each row publishes its token to pinned host memory; the host forms the accepted prefix.
+//   * in a verify step each row publishes its token (device memory and pinned host memory) and the workgroup
+//     that completes the step's last row forms the accepted prefix (a 64-bit step counter carries every row's
+//     draft mismatch bit), so `accepted` is in device memory for the consumers that follow on the stream.
 // Ticket counters and published bounds are reset by their last user, so launches replay from a captured graph
 // without memset nodes.
 #include "kls_internal.h"
@@ -843,15 +845,39 @@ __device__ int sample_tail(uint64_t lst, int kk, const SamplingParams p, double 
     return tok;
 }
 
+// Reports that an internal wait of this launch gave up (its results are then not trusted): the host turns a
+// nonzero word into an error.
+__device__ __forceinline__ void report_fault(const RowsArgs& a, uint32_t code) {
+    if (a.fault) __hip_atomic_store(a.fault, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Publishes row `row`'s token: device output, and for the host one 64-bit word (sequence number, token).
-// `seq` is the call's sequence number (call_seq, read ahead: the call block is host memory).
-__device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok, uint32_t seq) {
+// `seq` is the call's sequence number (call_seq, read ahead: the call block is host memory); `draft` the draft
+// this row's token is compared with in a verify step (src/engine.cpp:571: batch[row + 1]; unused for the last
+// row). Called by one lane.
+__device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok, uint32_t seq, int32_t draft) {
     a.out_tokens[row] = tok;
     a.row_ticket[row] = 0u;
     if (a.share_bounds) a.row_thr[row] = 0ull;
     if (a.host_res && row < VERIFY_MAX_ROWS)
         __hip_atomic_store(&a.host_res->row_word[row], ((uint64_t) seq << 32) | (uint32_t) tok, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_SYSTEM);
+    if (a.step_word) {
+        // engine.cpp:564-575: drafts are accepted while batch[i + 1] == t_i. Row r (< nb - 1) sets bit r when its
+        // token differs from its draft; bit nb - 1 stands for the end of the batch, so accepted = the lowest set
+        // bit of the union. The count in the high word tells the last row apart.
+        const uint64_t mine = (1ull << 32) | ((row + 1 < a.n_rows && tok != draft) ? (1ull << row) : 0ull);
+        const uint64_t prev = __hip_atomic_fetch_add(a.step_word, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t) (prev >> 32) == (uint32_t) (a.n_rows - 1)) {
+            const uint32_t bits = (uint32_t) (prev | mine) | (1u << (a.n_rows - 1));
+            const int acc = __builtin_ctz(bits);
+            *a.out_accepted = acc;
+            __hip_atomic_store(a.step_word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.host_res)
+                __hip_atomic_store(&a.host_res->step_word, ((uint64_t) seq << 32) | (uint32_t) acc, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
 }
 
 __device__ __forceinline__ uint32_t call_seq(const RowsArgs& a) { return a.host_res ? a.call->seq : 0u; }
@@ -925,6 +951,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     // what the row's last workgroup will need from host memory (the pinned call block, for graph-replayed
     // steps), read now so that its latency is hidden behind the segment's
     const uint32_t seq = call_seq(a);
+    const int32_t draft = (a.step_word && row + 1 < a.n_rows) ? a.call->drafts[row] : -1;
     const double u_row = GREEDY ? 0.0 : a.u[row];
     // greedy rows as std::max_element (engine.cpp:414): the running maximum starts at the first logit and only
     // '<' replaces it, so a NaN there is the result; otherwise the result is sampler.cpp's greedy id
@@ -1098,10 +1125,12 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         if (pen_lazy) {
             // table complete: every wave has counted (each does so right after issuing its loads, whatever the
             // others do, so the wait ends; the bound on it is a guard only)
-            for (int spin = 0; spin < (1 << 20); ++spin) {
-                if (__hip_atomic_load(&s_counted, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW) break;
-                __builtin_amdgcn_s_sleep(1);
+            bool counted = false;
+            for (int spin = 0; spin < a.spin_limit && !counted; ++spin) {
+                counted = __hip_atomic_load(&s_counted, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW;
+                if (!counted) __builtin_amdgcn_s_sleep(1);
             }
+            if (!counted && lane == 0) report_fault(a, FAULT_COUNT_WAIT);
             if (m1 > -INFINITY) {
                 const int off = 4 * ((s1 >> 2) * WG + tid) + (s1 & 3);
                 const uint32_t c = C16 ? (s_cnt[off >> 1] >> ((off & 1) << 4)) & 0xffffu : s_cnt[off];
@@ -1150,11 +1179,13 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                     }
                 }
             }
-            // (the bound on the wait is a guard only)
-            for (int spin = 0; spin < (1 << 20); ++spin) {
-                if (__hip_atomic_load(&s_qready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
-                __builtin_amdgcn_s_sleep(1);
+            // (the bound on the wait is a guard only: if it expires the launch reports a fault)
+            bool ready = false;
+            for (int spin = 0; spin < a.spin_limit && !ready; ++spin) {
+                ready = __hip_atomic_load(&s_qready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+                if (!ready) __builtin_amdgcn_s_sleep(1);
             }
+            if (!ready && lane == 0) report_fault(a, FAULT_BOUND_WAIT);
             gl = s_qe;
         }
         const uint32_t q = NW == 4 ? (uint32_t) rdlanei((int) gl, k - 1) : gl;  // all lanes active
@@ -1227,7 +1258,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                     a.dbg_meta[row * 2] = 0;
                     a.dbg_meta[row * 2 + 1] = 0;
                 }
-                publish(a, row, nan_first ? 0 : m ? key_id(m) : 0, seq);  // all -inf / NaN: id 0
+                publish(a, row, nan_first ? 0 : m ? key_id(m) : 0, seq, draft);  // all -inf / NaN: id 0
             }
             return;
         }
@@ -1258,7 +1289,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
         const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
                                     a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
-        if (lane == 0) publish(a, row, tok, seq);
+        if (lane == 0) publish(a, row, tok, seq, draft);
         return;
     }
     __syncthreads();
@@ -1283,7 +1314,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             a.dbg_meta[row * 2] = 0;
             a.dbg_meta[row * 2 + 1] = 0;
         }
-        publish(a, row, nan_first ? 0 : m ? key_id(m) : 0, seq);  // all -inf / NaN: id 0
+        publish(a, row, nan_first ? 0 : m ? key_id(m) : 0, seq, draft);  // all -inf / NaN: id 0
         return;
     }
 
@@ -1341,8 +1372,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
     const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
                                 a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
-    if (lane == 0) publish(a, row, tok, seq);
+    if (lane == 0) publish(a, row, tok, seq, draft);
 }
+
+__global__ void noop_kernel_impl(int) {}
 
 __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
     const long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
@@ -1572,6 +1605,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
     double* __restrict__ t = reinterpret_cast<double*>(w.keys + (int64_t) row * a.V);  // per-candidate terms
     const SamplingParams p = a.p;
     const uint32_t seq = call_seq(a);
+    const int32_t draft = (a.step_word && row + 1 < a.n_rows) ? a.call->drafts[row] : -1;
     auto img = [&](int i) { return (uint32_t) ((K[i] & vmask) >> ib); };  // value image, 0: NaN
     const uint32_t o0 = img(0);
     if (o0 == 0u) {  // no number in the row: the fast path's empty candidate list
@@ -1582,7 +1616,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
                     a.dbg_meta[row * 2] = 0;
                     a.dbg_meta[row * 2 + 1] = 0;
                 }
-                publish(a, row, 0, seq);
+                publish(a, row, 0, seq, draft);
             }
         }
         return;
@@ -1643,7 +1677,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
             a.dbg_meta[row * 2] = kk;
             a.dbg_meta[row * 2 + 1] = n;
         }
-        publish(a, row, tok, seq);
+        publish(a, row, tok, seq, draft);
     }
 }
 
@@ -1745,6 +1779,8 @@ hipError_t launch_sum_replay(const double* t, int n, double acc0, int mode, doub
     hipLaunchKernelGGL(sum_replay_kernel, dim3(1), dim3(TAIL_WG), 0, s, t, n, acc0, mode, thr, out);
     return hipGetLastError();
 }
+
+const void* noop_kernel() { return reinterpret_cast<const void*>(&noop_kernel_impl); }
 
 hipError_t launch_expf_table(uint32_t lo, long long n, float* out, hipStream_t s) {
     const int threads = 256;

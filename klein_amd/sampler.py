@@ -36,8 +36,12 @@ def _stream_ptr(stream):
 class Sampler:
     """klein::Sampler. max_rows bounds verify()/sample_batch() rows."""
 
-    def __init__(self, params: Params | None = None, n_vocab: int | None = None, max_rows: int = 16, **kw):
+    def __init__(self, params: Params | None = None, n_vocab: int | None = None, max_rows: int = 16,
+                 layout: dict | None = None, **kw):
+        """layout: launch-layout overrides for tests (kls_debug_set_layout): seg_len, target_wg, wide_target_wg,
+        share_min_wg, xcd_map. Results do not depend on them."""
         self._p = params if params is not None else Params(**kw)
+        self._layout = dict(layout or {})
         import random
         self._rng = MT19937_64(self._p.seed if self._p.seed else random.SystemRandom().getrandbits(32))
         self._h = None
@@ -61,9 +65,27 @@ class Sampler:
         _lib.check(L.kls_create(C.byref(cp), int(n_vocab), int(self._max_rows), C.byref(h)), "kls_create")
         self._h = h
         self._n_vocab = int(n_vocab)
+        if self._layout:
+            self.set_layout(**self._layout)
         for t in self._early:
             _lib.check(L.kls_accept(self._h, int(t)), "kls_accept")
         self._early = []
+
+    def set_layout(self, seg_len=0, target_wg=0, wide_target_wg=0, share_min_wg=0, xcd_map=-1, wait_limit=0):
+        """Test hook (kls_debug_set_layout): a field of 0 (xcd_map -1) keeps the default."""
+        lay = _lib.KlsDebugLayout(int(seg_len), int(target_wg), int(wide_target_wg), int(share_min_wg), int(xcd_map),
+                                  int(wait_limit))
+        _lib.check(_lib.lib().kls_debug_set_layout(self._h, C.byref(lay)), "kls_debug_set_layout")
+
+    def device_results(self):
+        """(d_tokens, d_accepted) device addresses of the last verify step's results (kls_device_results)."""
+        t, a = C.c_void_p(), C.c_void_p()
+        _lib.check(_lib.lib().kls_device_results(self._h, C.byref(t), C.byref(a)), "kls_device_results")
+        return t.value, a.value
+
+    def check(self):
+        """Raises if a kernel of this handle gave up an internal wait since the last check (kls_check)."""
+        _lib.check(_lib.lib().kls_check(self._h), "kls_check")
 
     def close(self):
         if self._h is not None:

@@ -29,18 +29,13 @@ def K():
 
 def run(torch, K, x, stride=None, max_rows=None, seg=None):
     """kls_argmax over the rows of x (optionally inside a wider row pitch); returns the indices."""
-    import os
     rows, V = x.shape
     pitch = stride or V
     buf = np.full((rows, pitch), np.float32(7e37), np.float32)  # (the pitch padding is never read)
     buf[:, :V] = x
     d = torch.from_numpy(buf).cuda()
-    if seg:
-        os.environ["KLS_SEG_LEN"] = str(seg)
-    try:
-        S = K.Sampler(W.Params(temperature=0.0), n_vocab=V, max_rows=max_rows or rows)
-    finally:
-        os.environ.pop("KLS_SEG_LEN", None)
+    S = K.Sampler(W.Params(temperature=0.0), n_vocab=V, max_rows=max_rows or rows,
+                  layout=dict(seg_len=seg) if seg else None)
     out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
     S.argmax(d[:, :V], out)
     torch.cuda.synchronize()

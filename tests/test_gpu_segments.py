@@ -2,9 +2,6 @@
 1024-thread workgroups over 16384..65536 ids with 16-bit history counts), of the 32-bit fallback for histories
 with 65536 or more ids in a row, and of verify steps wide enough to take the 1024-thread workgroups. Token ids
 and candidate lists bit-exact against the oracle."""
-import os
-from contextlib import contextmanager
-
 import numpy as np
 import pytest
 
@@ -31,21 +28,6 @@ def torch_cuda():
 def K():
     import klein_amd
     return klein_amd
-
-
-@contextmanager
-def seg_len(n):
-    """Segment length of the handles created inside (read by kls_create)."""
-    old = os.environ.get("KLS_SEG_LEN")
-    if n:
-        os.environ["KLS_SEG_LEN"] = str(n)
-    try:
-        yield
-    finally:
-        if old is None:
-            os.environ.pop("KLS_SEG_LEN", None)
-        else:
-            os.environ["KLS_SEG_LEN"] = old
 
 
 def dev(torch, a):
@@ -75,8 +57,7 @@ def check_batch(torch, K, O, x, p, hists, u, seg, label):
     off = np.zeros(rows + 1, np.int32)
     off[1:] = np.cumsum([len(h) for h in hists])
     ids = np.concatenate(hists).astype(np.int32) if off[-1] else np.zeros(1, np.int32)
-    with seg_len(seg):
-        S = K.Sampler(p, n_vocab=V, max_rows=rows)
+    S = K.Sampler(p, n_vocab=V, max_rows=rows, layout=dict(seg_len=seg) if seg else None)
     out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
     say(label, "seg", seg, "rows", rows, "V", V)
     S.sample_batch(dev(torch, x), dev(torch, u), out, dev(torch, off), dev(torch, ids))
