@@ -118,6 +118,22 @@ int kls_check(kls_handle h);
 int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t row_stride, const int32_t* d_hist_off,
                      const int32_t* d_hist_ids, const double* d_u, int32_t* d_out_tokens, kls_stream stream);
 
+/* No counterpart in the reference: kls_sample_batch for callers that cannot allocate (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc). It takes the parameters instead of a handle and
+ * allocates nothing: the sampling kernel's scratch (per (row, segment) candidate lists, per-row tickets and
+ * bounds, 515 KiB) is a static device array that each GPU holds for the life of the process, resolved with
+ * hipGetSymbolAddress on the first call with that device current. Same inputs, outputs and results as
+ * kls_sample_batch (stream NULL = the null stream). Limits: top-k at most 64 unless greedy (KLS_ERR_UNSUPPORTED
+ * otherwise), n_rows <= KLS_NOALLOC_MAX_ROWS and n_rows x segments <= KLS_NOALLOC_MAX_WORKGROUPS (segments of
+ * up to 65,536 ids: 4 per row at n_vocab = 248,320), else KLS_ERR_RANGE. Every call on one GPU shares the
+ * array: calls that overlap on one GPU (other streams, other threads) race and must be serialized by the
+ * caller; each call clears the rows' tickets and bounds with a small kernel before sampling. */
+#define KLS_NOALLOC_MAX_ROWS 256
+#define KLS_NOALLOC_MAX_WORKGROUPS 1024
+int kls_sample_batch_noalloc(const kls_params* params, int n_vocab, const float* d_logits, int n_rows,
+                             int64_t row_stride, const int32_t* d_hist_off, const int32_t* d_hist_ids,
+                             const double* d_u, int32_t* d_out_tokens, kls_stream stream);
+
 /* Replaces Engine::mtp_draft_token (src/engine.cpp:413-415): for each of n_rows rows of n_vocab f32 logits on
  * the device (row r at d_logits + r*row_stride), the index std::max_element returns: the first largest element
  * under '<', so a NaN never replaces the running maximum and a NaN first element is the result. Indices are

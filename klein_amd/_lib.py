@@ -19,7 +19,7 @@ KLS_ERR_OOM = 6
 
 # every entry point include/klein_sampler.h declares
 EXPORTS = ["kls_create", "kls_destroy", "kls_reset", "kls_accept", "kls_sample", "kls_verify", "kls_verify_enqueue",
-           "kls_verify_wait", "kls_sample_batch", "kls_argmax", "kls_ppl_scores",
+           "kls_verify_wait", "kls_sample_batch", "kls_sample_batch_noalloc", "kls_argmax", "kls_ppl_scores",
            "kls_device_results", "kls_check", "kls_get_candidates", "kls_debug_set_layout", "kls_debug_expf",
            "kls_debug_sum_replay", "kls_status_string", "kls_last_error"]
 
@@ -62,6 +62,8 @@ def lib():
         L.kls_verify_wait.argtypes = [P, I32P, I32P]
         L.kls_sample_batch.argtypes = [P, C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_void_p, C.c_void_p]
+        L.kls_sample_batch_noalloc.argtypes = [C.POINTER(KlsParams), C.c_int, C.c_void_p, C.c_int, C.c_int64,
+                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.kls_argmax.argtypes = [P, C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_void_p]
         L.kls_ppl_scores.argtypes = [P, C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_void_p, C.c_int64,
                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,

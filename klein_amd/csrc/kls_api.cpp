@@ -45,6 +45,52 @@ int fail(int status, const char* what, hipError_t e = hipSuccess) {
 
 }  // namespace
 
+namespace kls {
+
+int set_error(int status, const char* what, hipError_t e) { return fail(status, what, e); }
+
+// Segment length. First choice, for vocabularies of at least 16384 ids: 1024-thread workgroups over
+// 16384..65536 whole ids, the shortest that leaves at most 8 segments per row (the row's last workgroup then
+// merges the lists on one wave, without a barrier) and at most wide_target_wg workgroups (measured at V =
+// 248,320: 32768 ids for 1 to 16 rows, 8.6-10.1 µs against 8.9-14.4 µs with 8192-id segments; 65536 for the
+// 64-row batch). Greedy rows merge trivially and read faster from more workgroups, so they skip this choice.
+// Otherwise short segments (256 threads x {4, 8, 16, 32} logits): the smallest length whose grid
+// (rows x segments) stays within target_wg workgroups (128: half the CUs; every segment of a row then takes the
+// row's ticket, and more segments wait longer on it than their shorter reads save). When even 8192 ids leave
+// too many workgroups, 1024-thread workgroups over 16384..65536 ids (one per CU), the smallest length within
+// wide_target_wg: every logit and the row's history are then read once per segment with the chip full.
+void choose_segments(int V, int rows, bool greedy, int seg_override, int target_wg, int wide_target_wg, int* seg_len,
+                     int* segs) {
+    auto grid = [&](int sl) { return (long long) rows * ((V + sl - 1) / sl); };
+    int sl = SEG_MIN;
+    const int o = seg_override;
+    int few = 0;
+    for (int l = SEG_WIDE; l <= SEG_MAX && !few && !greedy; l *= 2)
+        if (V >= l && (V + l - 1) / l <= 8 && grid(l) <= wide_target_wg) few = l;
+    if (o >= SEG_MIN && o <= SEG_MAX && (o & (o - 1)) == 0) {
+        sl = o;
+    } else if (few) {
+        sl = few;
+    } else {
+        while (sl < SEG_WIDE / 2 && grid(sl) > target_wg) sl *= 2;
+        if (grid(sl) > target_wg) {
+            sl = SEG_WIDE;
+            while (sl < SEG_MAX && grid(sl) > wide_target_wg) sl *= 2;
+        }
+    }
+    *seg_len = sl;
+    *segs = (V + sl - 1) / sl;
+}
+
+SamplingParams sampling_params(const kls_params& p, int k) {
+    return SamplingParams{p.temperature, p.top_p, p.min_p, p.presence_penalty, p.frequency_penalty,
+                          p.repetition_penalty, std::min(k, KCAP), 1.0 / (double) p.repetition_penalty,
+                          (p.repetition_penalty >= 1.0f && p.presence_penalty >= 0.0f && p.frequency_penalty >= 0.0f)
+                              ? 1 : 0};
+}
+
+}  // namespace kls
+
 struct kls_sampler {
     kls_params p{};
     SamplingParams sp{};
@@ -53,7 +99,8 @@ struct kls_sampler {
     int V = 0, max_rows = 0, device = 0;
     int bucket_shift = MIN_BUCKET_SHIFT, n_buckets = 0;
     // launch layout (defaults; kls_debug_set_layout overrides them for tests)
-    int seg_len_override = 0, target_wg = 128, wide_target_wg = 320, share_min_wg = 1024, xcd_map = 1;
+    int seg_len_override = 0, target_wg = DEFAULT_TARGET_WG, wide_target_wg = DEFAULT_WIDE_TARGET_WG;
+    int share_min_wg = DEFAULT_SHARE_MIN_WG, xcd_map = 1;
     int spin_limit = DEFAULT_SPIN_LIMIT;
     hipStream_t stream = nullptr;  // the library's stream of this device (shared by handles; not destroyed)
     // ordering of launches that share the scratch: the stream of the last launch, and an event that makes a
@@ -193,36 +240,8 @@ hipError_t prepare_graph_stream(int device, hipStream_t s) {
     return hipSuccess;
 }
 
-// Segment length. First choice, for vocabularies of at least 16384 ids: 1024-thread workgroups over
-// 16384..65536 whole ids, the shortest that leaves at most 8 segments per row (the row's last workgroup then
-// merges the lists on one wave, without a barrier) and at most wide_target_wg workgroups (measured at V =
-// 248,320: 32768 ids for 1 to 16 rows, 8.6-10.1 µs against 8.9-14.4 µs with 8192-id segments; 65536 for the
-// 64-row batch). Greedy rows merge trivially and read faster from more workgroups, so they skip this choice.
-// Otherwise short segments (256 threads x {4, 8, 16, 32} logits): the smallest length whose grid
-// (rows x segments) stays within target_wg workgroups (128: half the CUs; every segment of a row then takes the
-// row's ticket, and more segments wait longer on it than their shorter reads save). When even 8192 ids leave
-// too many workgroups, 1024-thread workgroups over 16384..65536 ids (one per CU), the smallest length within
-// wide_target_wg: every logit and the row's history are then read once per segment with the chip full.
 void segments_for(const kls_sampler* h, int rows, bool greedy, int* seg_len, int* segs) {
-    auto grid = [&](int sl) { return (long long) rows * ((h->V + sl - 1) / sl); };
-    int sl = SEG_MIN;
-    const int o = h->seg_len_override;
-    int few = 0;
-    for (int l = SEG_WIDE; l <= SEG_MAX && !few && !greedy; l *= 2)
-        if (h->V >= l && (h->V + l - 1) / l <= 8 && grid(l) <= h->wide_target_wg) few = l;
-    if (o >= SEG_MIN && o <= SEG_MAX && (o & (o - 1)) == 0) {
-        sl = o;
-    } else if (few) {
-        sl = few;
-    } else {
-        while (sl < SEG_WIDE / 2 && grid(sl) > h->target_wg) sl *= 2;
-        if (grid(sl) > h->target_wg) {
-            sl = SEG_WIDE;
-            while (sl < SEG_MAX && grid(sl) > h->wide_target_wg) sl *= 2;
-        }
-    }
-    *seg_len = sl;
-    *segs = (h->V + sl - 1) / sl;
+    choose_segments(h->V, rows, greedy, h->seg_len_override, h->target_wg, h->wide_target_wg, seg_len, segs);
 }
 
 // Rebuilds the device history from the host counts (bucketed unique ids + counts) and clears `pending`.
@@ -518,11 +537,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     h->wide = wide;
     h->penalize = params->presence_penalty != 0.0f || params->frequency_penalty != 0.0f ||
                   params->repetition_penalty != 1.0f;
-    h->sp = SamplingParams{params->temperature, params->top_p, params->min_p, params->presence_penalty,
-                           params->frequency_penalty, params->repetition_penalty, std::min(k, KCAP),
-                           1.0 / (double) params->repetition_penalty,
-                           (params->repetition_penalty >= 1.0f && params->presence_penalty >= 0.0f &&
-                            params->frequency_penalty >= 0.0f) ? 1 : 0};
+    h->sp = sampling_params(*params, k);
     while (((n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift) > MAX_BUCKETS) h->bucket_shift++;
     h->n_buckets = (n_vocab + (1 << h->bucket_shift) - 1) >> h->bucket_shift;
     (void) hipGetDevice(&h->device);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "klein_sampler.h"
+
 namespace kls {
 
 // Candidates kept per segment and per row on the fast path (one per lane of a wave64).
@@ -153,6 +155,18 @@ struct PplArgs {
     double* out_nll_base;
     int32_t* out_base_top;
 };
+// The launch layout of rows_kernel for `rows` rows of V ids (kls_api.cpp): ids per segment and segments per row.
+// seg_override (a power of two in [SEG_MIN, SEG_MAX], else 0) forces the length; target_wg and wide_target_wg
+// are the grid sizes the choice aims at (defaults 128 and 320).
+void choose_segments(int V, int rows, bool greedy, int seg_override, int target_wg, int wide_target_wg, int* seg_len,
+                     int* segs);
+constexpr int DEFAULT_TARGET_WG = 128, DEFAULT_WIDE_TARGET_WG = 320;
+// Grids of more (row, segment) workgroups than this share per-row running bounds through device memory.
+constexpr int DEFAULT_SHARE_MIN_WG = 1024;
+// Records the failure for kls_last_error (kls_api.cpp) and returns `status`.
+int set_error(int status, const char* what, hipError_t e = hipSuccess);
+// The kernel's parameter block for klein::SamplerParams p with effective top-k k (src/sampler.cpp:42).
+SamplingParams sampling_params(const kls_params& p, int k);
 int ppl_segments(int V, int rows, int* seg_len);  // segments per row (and their length) of a launch
 hipError_t launch_ppl(const PplArgs& a, hipStream_t s);
 

@@ -74,3 +74,24 @@ def test_no_device_is_reported_without_gpu():
     h = C.c_void_p()
     p = _params()
     assert L.kls_create(C.byref(p), 1000, 4, C.byref(h)) == _lib.KLS_ERR_NO_DEVICE
+
+
+def test_noalloc_limits_reported_before_device_work():
+    """kls_sample_batch_noalloc refuses what its static scratch cannot hold, before any HIP call (so also without a
+    GPU): rows above KLS_NOALLOC_MAX_ROWS, rows x segments above KLS_NOALLOC_MAX_WORKGROUPS, top-k above 64."""
+    L = _lib.lib()
+    fake = C.c_void_p(0x1000)  # never dereferenced: the checks come first
+    p = _params(top_k=20)
+    args = lambda rows, V: (C.byref(p), V, fake, rows, V, None, None, fake, fake, None)  # noqa: E731
+    assert L.kls_sample_batch_noalloc(*args(257, 248320)) == _lib.KLS_ERR_RANGE
+    assert L.kls_sample_batch_noalloc(*args(256, 65536 * 5)) == _lib.KLS_ERR_RANGE
+    pw = _params(top_k=65)
+    assert L.kls_sample_batch_noalloc(C.byref(pw), 1000, fake, 1, 1000, None, None, fake, fake, None) == \
+        _lib.KLS_ERR_UNSUPPORTED
+    pn = _params(top_k=0)
+    assert L.kls_sample_batch_noalloc(C.byref(pn), 1000, fake, 1, 1000, None, None, fake, fake, None) == \
+        _lib.KLS_ERR_UNSUPPORTED
+    assert L.kls_sample_batch_noalloc(None, 1000, fake, 1, 1000, None, None, fake, fake, None) == \
+        _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_sample_batch_noalloc(C.byref(p), 1000, fake, 1, 999, None, None, fake, fake, None) == \
+        _lib.KLS_ERR_INVALID_ARG
