@@ -157,6 +157,49 @@ int kls_ppl_scores(kls_handle h, const float* d_logits, int n_rows, int64_t row_
                    const float* d_base, int64_t base_stride, double* d_lse, double* d_nll, int32_t* d_top,
                    double* d_kl, double* d_nll_base, int32_t* d_base_top, kls_stream stream);
 
+/* ---- The verify step's consumer: the recurrent-state rollback (src/engine.cpp:578-583, src/state.cpp:162-184).
+ *
+ * Storage type of the rollback snapshots (StateConfig::snap_type, src/state.h:20). */
+enum kls_snap_type { KLS_SNAP_F32 = 0, KLS_SNAP_F16 = 1, KLS_SNAP_BF16 = 2 };
+
+/* The Gated DeltaNet recurrent state of one sequence as klein's State lays it out (src/state.h:45-46,
+ * src/state.cpp:68-76), for each of n_layers recurrent layers l:
+ *   conv[l]      n_snapshots slots of conv_row f32, slot i at byte offset i * conv_stride: slot 0 the current
+ *                state, slot s the state s tokens back;
+ *   ssm[l]       ssm_row f32: the current state;
+ *   ssm_snap[l]  n_snapshots - 1 rows of ssm_row elements of snap_type, row i at byte offset i * snap_stride:
+ *                row s - 1 the state s tokens back (unused when n_snapshots is 1).
+ * The three arrays are host arrays of n_layers device pointers; the strides are ggml's nb[1]. */
+typedef struct kls_recurrent_desc {
+    int32_t n_layers;
+    int32_t n_snapshots;
+    int64_t conv_row;
+    int64_t ssm_row;
+    int64_t conv_stride;
+    int64_t snap_stride;
+    int32_t snap_type;
+    float* const* conv;
+    float* const* ssm;
+    const void* const* ssm_snap;
+} kls_recurrent_desc;
+
+typedef struct kls_recurrent* kls_recurrent_handle;
+
+/* No counterpart in the reference (its State owns the tensors): copies the layer pointer table to device
+ * memory (the only allocation) for kls_rollback_recurrent. The state buffers stay the caller's. */
+int kls_recurrent_create(const kls_recurrent_desc* desc, kls_recurrent_handle* out);
+int kls_recurrent_destroy(kls_recurrent_handle r);
+
+/* Replaces `rejected = (nb - 1) - accepted; if (rejected > 0) state->rollback_recurrent(gpu, rejected)` of
+ * Engine::generate (src/engine.cpp:580-583) with State::rollback_recurrent (src/state.cpp:162-184): for every
+ * layer, conv slot s is copied over slot 0 and snapshot row s - 1 is converted to f32 into ssm, s = rejected.
+ * `accepted` is read from device memory (d_accepted: kls_device_results's, or any device int32) by the kernel,
+ * so the call can be enqueued right after kls_verify_enqueue on the same stream, before the host knows the
+ * result. One kernel launch over all layers, asynchronous on `stream` (NULL: the null stream). nb must not
+ * exceed n_snapshots (KLS_ERR_RANGE; the reference asserts s < n_snapshots); an accepted value outside
+ * [0, nb - 1] rolls nothing back. */
+int kls_rollback_recurrent(kls_recurrent_handle r, const int32_t* d_accepted, int nb, kls_stream stream);
+
 /* The sorted top-k candidates of `row` from the last completed call (kls_sample: row 0): ids, softmax
  * probabilities before min-p/top-p truncation (up to `cap`), k, and how many survived min-p/top-p.
  * Synchronizes the handle's stream. For tests and tooling; not needed on the sampling path. */

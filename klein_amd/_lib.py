@@ -20,7 +20,8 @@ KLS_ERR_OOM = 6
 # every entry point include/klein_sampler.h declares
 EXPORTS = ["kls_create", "kls_destroy", "kls_reset", "kls_accept", "kls_sample", "kls_verify", "kls_verify_enqueue",
            "kls_verify_wait", "kls_sample_batch", "kls_sample_batch_noalloc", "kls_argmax", "kls_ppl_scores",
-           "kls_device_results", "kls_check", "kls_get_candidates", "kls_debug_set_layout", "kls_debug_expf",
+           "kls_device_results", "kls_check", "kls_recurrent_create", "kls_recurrent_destroy",
+           "kls_rollback_recurrent", "kls_get_candidates", "kls_debug_set_layout", "kls_debug_expf",
            "kls_debug_sum_replay", "kls_status_string", "kls_last_error"]
 
 
@@ -33,6 +34,16 @@ class KlsParams(C.Structure):
 class KlsDebugLayout(C.Structure):
     _fields_ = [("seg_len", C.c_int32), ("target_wg", C.c_int32), ("wide_target_wg", C.c_int32),
                 ("share_min_wg", C.c_int32), ("xcd_map", C.c_int32), ("wait_limit", C.c_int32)]
+
+
+class KlsRecurrentDesc(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("n_snapshots", C.c_int32), ("conv_row", C.c_int64),
+                ("ssm_row", C.c_int64), ("conv_stride", C.c_int64), ("snap_stride", C.c_int64),
+                ("snap_type", C.c_int32), ("conv", C.POINTER(C.c_void_p)), ("ssm", C.POINTER(C.c_void_p)),
+                ("ssm_snap", C.POINTER(C.c_void_p))]
+
+
+KLS_SNAP_F32, KLS_SNAP_F16, KLS_SNAP_BF16 = 0, 1, 2
 
 
 class KlsError(RuntimeError):
@@ -64,6 +75,9 @@ def lib():
                                        C.c_void_p, C.c_void_p]
         L.kls_sample_batch_noalloc.argtypes = [C.POINTER(KlsParams), C.c_int, C.c_void_p, C.c_int, C.c_int64,
                                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.kls_recurrent_create.argtypes = [C.POINTER(KlsRecurrentDesc), C.POINTER(C.c_void_p)]
+        L.kls_recurrent_destroy.argtypes = [P]
+        L.kls_rollback_recurrent.argtypes = [P, C.c_void_p, C.c_int, C.c_void_p]
         L.kls_argmax.argtypes = [P, C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_void_p]
         L.kls_ppl_scores.argtypes = [P, C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_void_p, C.c_int64,
                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,

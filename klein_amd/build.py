@@ -11,7 +11,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libklein_sampler.so")
-SOURCES = ["kls_kernels.hip", "kls_sort.hip", "kls_ppl.hip", "kls_noalloc.hip", "kls_api.cpp", "sampler.cpp"]
+SOURCES = ["kls_kernels.hip", "kls_sort.hip", "kls_ppl.hip", "kls_noalloc.hip", "kls_state.hip", "kls_api.cpp", "sampler.cpp"]
 ARCH = os.environ.get("KLS_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

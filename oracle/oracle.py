@@ -216,3 +216,37 @@ class RefSampler:
         toks = np.zeros(nb, dtype=np.int32)
         acc = self._L.ref_verify(self._h, _fp(lg), V, nb, _ip(dr), _ip(toks))
         return toks, int(acc)
+
+
+# ---- The verify step's consumer: the recurrent-state rollback (src/engine.cpp:578-583, src/state.cpp:162-184).
+
+SNAP_F32, SNAP_F16, SNAP_BF16 = 0, 1, 2
+
+
+def snap_to_f32(row: np.ndarray, snap_type: int) -> np.ndarray:
+    """ggml_cpy of a snapshot row to f32 (src/state.cpp:178): f32 unchanged; f16 (uint16 bit patterns) through
+    numpy's binary16 conversion; bf16 (uint16 bit patterns) as the high half of the f32 bits. All exact."""
+    if snap_type == SNAP_F32:
+        return np.array(row, dtype=np.float32)
+    u = np.asarray(row, dtype=np.uint16)
+    if snap_type == SNAP_F16:
+        return u.view(np.float16).astype(np.float32)
+    return (u.astype(np.uint32) << 16).view(np.float32)
+
+
+def rollback_recurrent(conv: np.ndarray, ssm: np.ndarray, snap: np.ndarray | None, snap_type: int, accepted: int,
+                       nb: int):
+    """One layer of Engine::generate's rollback: rejected = (nb - 1) - accepted (src/engine.cpp:580), then
+    State::rollback_recurrent(gpu, rejected) (src/state.cpp:162-184): nothing for s <= 0, else conv slot s over
+    slot 0 (state.cpp:177) and snapshot row s - 1 converted into ssm (state.cpp:178). conv: [n_snapshots, conv_row]
+    f32; ssm: [ssm_row] f32; snap: [n_snapshots - 1, ssm_row] (f32, or uint16 bits of f16 / bf16). Returns the new
+    (conv, ssm) as copies."""
+    conv = np.array(conv, dtype=np.float32, copy=True)
+    ssm = np.array(ssm, dtype=np.float32, copy=True)
+    s = (nb - 1) - accepted
+    if s <= 0:
+        return conv, ssm
+    assert s < conv.shape[0], "state.cpp:164: s < n_snapshots"
+    conv[0] = conv[s]
+    ssm[:] = snap_to_f32(snap[s - 1], snap_type)
+    return conv, ssm

@@ -95,3 +95,25 @@ def test_noalloc_limits_reported_before_device_work():
         _lib.KLS_ERR_INVALID_ARG
     assert L.kls_sample_batch_noalloc(C.byref(p), 1000, fake, 1, 999, None, None, fake, fake, None) == \
         _lib.KLS_ERR_INVALID_ARG
+
+
+def test_recurrent_desc_errors_before_device_work():
+    L = _lib.lib()
+    h = C.c_void_p()
+    P = C.c_void_p * 2
+    arr = P(0x1000, 0x2000)
+    ptr = C.cast(arr, C.POINTER(C.c_void_p))
+    ok = dict(n_layers=2, n_snapshots=4, conv_row=64, ssm_row=128, conv_stride=256, snap_stride=256,
+              snap_type=_lib.KLS_SNAP_F16, conv=ptr, ssm=ptr, ssm_snap=ptr)
+
+    def make(**kw):
+        d = dict(ok)
+        d.update(kw)
+        return _lib.KlsRecurrentDesc(*[d[f] for f, _ in _lib.KlsRecurrentDesc._fields_])
+
+    assert L.kls_recurrent_create(None, C.byref(h)) == _lib.KLS_ERR_INVALID_ARG
+    for bad in (dict(n_layers=0), dict(n_snapshots=0), dict(snap_type=7), dict(conv_stride=128),
+                dict(snap_stride=100), dict(conv=None), dict(ssm_snap=None)):
+        assert L.kls_recurrent_create(C.byref(make(**bad)), C.byref(h)) == _lib.KLS_ERR_INVALID_ARG, bad
+    assert L.kls_rollback_recurrent(None, None, 4, None) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_recurrent_destroy(None) == _lib.KLS_ERR_INVALID_ARG

@@ -334,3 +334,60 @@ def test_golden_fixtures(oracle_lib, name):
         assert list(ids) == case["topk_ids"]
         assert [float(x) for x in probs] == case["topk_probs"]
         assert kept == case["kept"]
+
+
+def _decode_binary16(u):
+    """IEEE binary16 decoded from its fields with integer arithmetic (sign, 5-bit exponent, 10-bit fraction)."""
+    sgn = -1.0 if u >> 15 else 1.0
+    e, f = (u >> 10) & 0x1F, u & 0x3FF
+    if e == 0:
+        return sgn * f * 2.0 ** -24
+    if e == 31:
+        return sgn * float("inf") if f == 0 else float("nan")
+    return sgn * (1024 + f) * 2.0 ** (e - 25)
+
+
+def _decode_bfloat16(u):
+    """bfloat16 decoded from its fields (sign, 8-bit exponent, 7-bit fraction)."""
+    sgn = -1.0 if u >> 15 else 1.0
+    e, f = (u >> 7) & 0xFF, u & 0x7F
+    if e == 0:
+        return sgn * f * 2.0 ** -133
+    if e == 255:
+        return sgn * float("inf") if f == 0 else float("nan")
+    return sgn * (128 + f) * 2.0 ** (e - 134)
+
+
+def test_snapshot_conversions_every_pattern(oracle_lib):
+    """The oracle's f16 / bf16 -> f32 conversion of rollback snapshots against a field-by-field decode, on all
+    65,536 bit patterns each (NaN patterns: NaN out)."""
+    O = oracle_lib
+    pats = np.arange(65536, dtype=np.uint32)
+    for st, dec in ((O.SNAP_F16, _decode_binary16), (O.SNAP_BF16, _decode_bfloat16)):
+        got = O.snap_to_f32(pats.astype(np.uint16), st)
+        want = np.array([dec(int(u)) for u in pats], dtype=np.float64)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].astype(np.float64), want[~nan])
+
+
+def test_rollback_closed_form(oracle_lib):
+    """Slot i of conv holds 100 + i and snapshot row j holds (j + 1) / 2 (states i and j + 1 tokens back,
+    src/state.h:45-46): rolling back after `accepted` of nb - 1 drafts leaves 100 + s in slot 0 and s / 2 in ssm,
+    s = nb - 1 - accepted, the other slots untouched; s = 0 changes nothing."""
+    O = oracle_lib
+    nb, conv_row, ssm_row = 4, 6, 5
+    conv = np.stack([np.full(conv_row, 100 + i, np.float32) for i in range(nb)])
+    ssm = np.full(ssm_row, -7.0, np.float32)
+    for st, enc in ((O.SNAP_F32, lambda v: np.float32(v)),
+                    (O.SNAP_F16, lambda v: np.float16(v).view(np.uint16)),
+                    (O.SNAP_BF16, lambda v: np.uint16(np.float32(v).view(np.uint32) >> 16))):
+        snap = np.stack([np.full(ssm_row, enc((j + 1) / 2)) for j in range(nb - 1)])
+        for acc in range(nb):
+            c, m = O.rollback_recurrent(conv, ssm, snap, st, acc, nb)
+            s = nb - 1 - acc
+            assert np.all(c[1:] == conv[1:])
+            if s == 0:
+                assert np.all(c == conv) and np.all(m == ssm)
+            else:
+                assert np.all(c[0] == 100 + s) and np.all(m == s / 2)
