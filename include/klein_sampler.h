@@ -227,6 +227,13 @@ typedef struct kls_debug_layout {
 } kls_debug_layout;
 int kls_debug_set_layout(kls_handle h, const kls_debug_layout* layout);
 
+/* Measurement hook, no counterpart in the reference: device time of the verify kernel as the last verify step's
+ * graph runs it (same arguments: uniforms and drafts from the pinned call block, results published to pinned
+ * memory), measured with HIP events on `stream` around `reps` launches of a graph of n back-to-back copies;
+ * *out_us = microseconds per kernel. Needs a completed verify step on the handle (KLS_ERR_INVALID_ARG otherwise);
+ * the handle's results are those of that step again afterwards. */
+int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, double* out_us);
+
 /* Test hook, no counterpart in the reference: the wide top-k tail's parallel replay of a sequential double sum
  * (src/sampler.cpp:58,70-77,84-87 accumulate this way) over the n device doubles d_terms from acc0:
  * acc = acc + d_terms[i] in order, stopping after the first i where (mode 1) acc >= thr or (mode 2) acc <= 0

@@ -155,6 +155,7 @@ struct kls_sampler {
     int g_rows = 0;
     bool g_count_wide = false;
     bool g_valid = false;
+    RowsArgs g_args{};  // the arguments the verify graph was captured with
 };
 
 namespace {
@@ -412,6 +413,7 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
             h->g_logits = dl;
             h->g_rows = rows;
             h->g_count_wide = h->count_wide;
+            h->g_args = a;
             h->g_valid = true;
         }
         KLS_HIP(prepare_graph_stream(h->device, s));
@@ -813,6 +815,47 @@ int kls_get_candidates(kls_handle h, int row, int32_t* ids, float* probs, int ca
     if (n_k) *n_k = meta[0];
     if (n_kept) *n_kept = meta[1];
     return KLS_OK;
+}
+
+int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, double* out_us) {
+    if (int st = check_handle(h)) return st;
+    if (n < 1 || reps < 1 || !out_us) return fail(KLS_ERR_INVALID_ARG, "bad arguments");
+    if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is in flight on this handle");
+    if (!h->g_valid) return fail(KLS_ERR_INVALID_ARG, "no captured verify step on this handle");
+    (void) hipSetDevice(h->device);
+    hipStream_t s = stream ? (hipStream_t) stream : h->stream;
+    if (int st = order_on(h, s)) return st;
+    // n launches of the verify kernel with the captured step's arguments, captured back to back in one graph
+    hipStream_t cap = nullptr;
+    KLS_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+    hipError_t e = hipStreamBeginCapture(cap, hipStreamCaptureModeRelaxed);
+    for (int i = 0; i < n && e == hipSuccess; ++i) e = launch_rows(h->g_args, h->greedy, h->penalize, cap);
+    hipGraph_t g = nullptr;
+    const hipError_t ce = hipStreamEndCapture(cap, &g);
+    (void) hipStreamDestroy(cap);
+    if (e != hipSuccess) return fail(KLS_ERR_HIP, "launch_rows (capture)", e);
+    if (ce != hipSuccess) return fail(KLS_ERR_HIP, "hipStreamEndCapture", ce);
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void) hipGraphDestroy(g);
+    if (e != hipSuccess) return fail(KLS_ERR_HIP, "hipGraphInstantiate", e);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = prepare_graph_stream(h->device, s);
+    if (e == hipSuccess) e = hipGraphLaunch(x, s);  // (once untimed)
+    if (e == hipSuccess) e = hipEventRecord(e0, s);
+    for (int r = 0; r < reps && e == hipSuccess; ++r) e = hipGraphLaunch(x, s);
+    if (e == hipSuccess) e = hipEventRecord(e1, s);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) (void) hipEventDestroy(e0);
+    if (e1) (void) hipEventDestroy(e1);
+    (void) hipGraphExecDestroy(x);
+    if (e != hipSuccess) return fail(KLS_ERR_HIP, "timed replay", e);
+    *out_us = (double) ms * 1e3 / ((double) n * reps);
+    return check_fault(h);
 }
 
 int kls_debug_sum_replay(const double* d_terms, int n, double acc0, int mode, double thr, double* d_out,

@@ -852,16 +852,15 @@ __device__ __forceinline__ void report_fault(const RowsArgs& a, uint32_t code) {
 }
 
 // Publishes row `row`'s token: device output, and for the host one 64-bit word (sequence number, token).
-// `seq` is the call's sequence number (call_seq, read ahead: the call block is host memory); `draft` the draft
+// `seq` is the call's sequence number (read_call: the call block is host memory); `draft` the draft
 // this row's token is compared with in a verify step (src/engine.cpp:571: batch[row + 1]; unused for the last
 // row). Called by one lane.
 __device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok, uint32_t seq, int32_t draft) {
     a.out_tokens[row] = tok;
     a.row_ticket[row] = 0u;
     if (a.share_bounds) a.row_thr[row] = 0ull;
-    if (a.host_res && row < VERIFY_MAX_ROWS)
-        __hip_atomic_store(&a.host_res->row_word[row], ((uint64_t) seq << 32) | (uint32_t) tok, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_SYSTEM);
+    // (the step counter first: waiting for its return then does not wait for a store to host memory)
+    int acc = -1;
     if (a.step_word) {
         // engine.cpp:564-575: drafts are accepted while batch[i + 1] == t_i. Row r (< nb - 1) sets bit r when its
         // token differs from its draft; bit nb - 1 stands for the end of the batch, so accepted = the lowest set
@@ -869,18 +868,43 @@ __device__ __forceinline__ void publish(const RowsArgs& a, int row, int tok, uin
         const uint64_t mine = (1ull << 32) | ((row + 1 < a.n_rows && tok != draft) ? (1ull << row) : 0ull);
         const uint64_t prev = __hip_atomic_fetch_add(a.step_word, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if ((uint32_t) (prev >> 32) == (uint32_t) (a.n_rows - 1)) {
-            const uint32_t bits = (uint32_t) (prev | mine) | (1u << (a.n_rows - 1));
-            const int acc = __builtin_ctz(bits);
+            acc = __builtin_ctz((uint32_t) (prev | mine) | (1u << (a.n_rows - 1)));
             *a.out_accepted = acc;
             __hip_atomic_store(a.step_word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (a.host_res)
-                __hip_atomic_store(&a.host_res->step_word, ((uint64_t) seq << 32) | (uint32_t) acc, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_SYSTEM);
         }
+    }
+    if (a.host_res && row < VERIFY_MAX_ROWS) {
+        __hip_atomic_store(&a.host_res->row_word[row], ((uint64_t) seq << 32) | (uint32_t) tok, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        if (acc >= 0)
+            __hip_atomic_store(&a.host_res->step_word, ((uint64_t) seq << 32) | (uint32_t) acc, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
-__device__ __forceinline__ uint32_t call_seq(const RowsArgs& a) { return a.host_res ? a.call->seq : 0u; }
+// What a row's last workgroup needs from the call block (pinned host memory for steps over the handle's history):
+// the sequence number to publish, the row's draft and uniform. The workgroup's last wave reads them (scalar
+// loads) once it has issued all its logit loads, and hands them to wave 0 through LDS before a barrier that
+// precedes the tail. Issued at kernel start, the same loads held the workgroup's first barrier (whose wait on the
+// scalar/LDS counter includes them) for a PCIe round trip before most logits were requested; as system-scope
+// vector loads they were slower still. Measured on the 4-row verify step: 14.1 us at kernel start, 9.8 us here,
+// 9.6 us with no host reads at all.
+struct CallIn {
+    uint32_t seq;
+    int32_t draft;
+    double u;
+};
+
+__shared__ CallIn s_cin;
+
+template <bool GREEDY>
+__device__ __forceinline__ CallIn read_call(const RowsArgs& a, int row) {
+    CallIn c{0u, -1, 0.0};
+    if (a.host_res) c.seq = a.call->seq;
+    if (a.step_word && row + 1 < a.n_rows) c.draft = a.call->drafts[row];
+    if (!GREEDY) c.u = a.u[row];
+    return c;
+}
 
 // Loads this thread's logits of groups I0 <= i < I1: ids lb + 4*(i*WG + tid) + e.
 //  * FULL: every group is a whole aligned float4 inside the row, read through the buffer resource `seg` (base =
@@ -919,7 +943,6 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     constexpr int WG = NW * 64;
     constexpr int SEG = WG * EPT;
     constexpr int NV = EPT / 4;    // float4 per thread
-    constexpr int NVH = NV / 2;    // float4 loaded before the history prefetch
     constexpr bool C16 = NW > 4;   // 16-bit history counts (segments of 16384 ids and more)
     static_assert(NW == 4 || NW == 16, "workgroup width");
     static_assert(!C16 || NV % 2 == 0, "half-segment windows");
@@ -950,9 +973,6 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     uint64_t* seg_out = a.seg_cand + ((int64_t) row * a.segs + seg) * KCAP;
     // what the row's last workgroup will need from host memory (the pinned call block, for graph-replayed
     // steps), read now so that its latency is hidden behind the segment's
-    const uint32_t seq = call_seq(a);
-    const int32_t draft = (a.step_word && row + 1 < a.n_rows) ? a.call->drafts[row] : -1;
-    const double u_row = GREEDY ? 0.0 : a.u[row];
     // greedy rows as std::max_element (engine.cpp:414): the running maximum starts at the first logit and only
     // '<' replaces it, so a NaN there is the result; otherwise the result is sampler.cpp's greedy id
     const float l0 = (GREEDY && a.first_nan) ? L[0] : 0.0f;
@@ -1040,6 +1060,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         __syncthreads();  // counters cleared
     }
     load_groups<FULL, WG, EPT, Q3, NV>(v, vec, seg_rsrc, L, lb, hi);
+    const CallIn cin = wave == NW - 1 ? read_call<GREEDY>(a, row) : CallIn{0u, -1, 0.0};  // (to LDS below)
     // with penalties (16-bit or narrow tables) the counts are applied group by group as the logits are first
     // used (or lazily), below; wide counts are applied here, half a segment at a time
     const bool pen_now = PENALIZE && !wide && !a.p.lazy;
@@ -1089,6 +1110,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         uint64_t key = best_v > -INFINITY ? mk_key(best_v, best_id) : 0ull;
         key = wave_max64(key, lane);
         if (lane == 0) s_red<NW>[wave] = key;
+        if (wave == NW - 1 && lane == 0) s_cin = cin;
         __syncthreads();
         if (tid == 0) {
             uint64_t m = s_red<NW>[0];
@@ -1228,6 +1250,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             __builtin_amdgcn_wave_barrier();
         }
         uint64_t lst;
+        if (wave == NW - 1 && lane == 0) s_cin = cin;  // (read by wave 0 after wg_select's barrier)
         if (!wg_select<NW>(w, lane, wave, &lst))
             lst = segment_slow<NW, SEG, C16>(a, L, row, lo, hi, lb, PENALIZE, wide, rh, t_row, lane, wave);
         if (wave == 0) {
@@ -1246,6 +1269,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     const uint64_t* cand = a.seg_cand + (int64_t) row * a.segs * KCAP;
     if (GREEDY ? a.segs <= 64 : a.segs <= 8) {
         if (wave != 0) return;
+        const CallIn c0 = s_cin;
+        const uint32_t seq = c0.seq;
+        const int32_t draft = c0.draft;
+        const double u_row = c0.u;
         wait_stores();
         uint32_t prev = 0u;
         if (lane == 0) prev = atomicAdd(&a.row_ticket[row], 1u);
@@ -1300,6 +1327,10 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
+    const CallIn c0 = s_cin;
+    const uint32_t seq = c0.seq;
+    const int32_t draft = c0.draft;
+    const double u_row = c0.u;
 
     if (GREEDY) {
         uint64_t m = 0ull;
@@ -1604,8 +1635,9 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
     const uint64_t* __restrict__ K = w.sorted + (int64_t) row * a.V;
     double* __restrict__ t = reinterpret_cast<double*>(w.keys + (int64_t) row * a.V);  // per-candidate terms
     const SamplingParams p = a.p;
-    const uint32_t seq = call_seq(a);
-    const int32_t draft = (a.step_word && row + 1 < a.n_rows) ? a.call->drafts[row] : -1;
+    const CallIn cin = read_call<false>(a, row);
+    const uint32_t seq = cin.seq;
+    const int32_t draft = cin.draft;
     auto img = [&](int i) { return (uint32_t) ((K[i] & vmask) >> ib); };  // value image, 0: NaN
     const uint32_t o0 = img(0);
     if (o0 == 0u) {  // no number in the row: the fast path's empty candidate list
@@ -1659,7 +1691,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
     }
     // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a chain
     // of additions of -p_i (exactly the subtractions)
-    const double r0 = __dadd_rn(__dmul_rn(a.u[row], __dsub_rn(total, 0.0)), 0.0);
+    const double r0 = __dadd_rn(__dmul_rn(cin.u, __dsub_rn(total, 0.0)), 0.0);
     const bool act = lane < kk;
     const float dbg_p = act ? (float) t[lane] : 0.0f;
     __syncthreads();  // (every thread has read its p_i for the debug copy)
