@@ -103,6 +103,32 @@ __device__ __forceinline__ void wait_stores() {
 }
 __device__ __forceinline__ uint64_t min64(uint64_t a, uint64_t b) { return a > b ? b : a; }
 
+// Signalling between the waves of one workgroup through LDS flags and counters. The LDS serves each wave's
+// operations in order, so the LDS writes a wave made before raising a flag are seen by a wave that has seen the
+// flag and reads after it. Release or acquire orderings at workgroup scope would also make the wave wait for its
+// outstanding global loads (s_waitcnt vmcnt(0)), which drains a stream of logit loads still in flight; these wait
+// for the wave's LDS operations only (lgkmcnt(0)) and keep the compiler from moving memory operations across.
+__device__ __forceinline__ void lds_wait() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt not waited for
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ int lds_raise(int* p, int v) {
+    lds_wait();
+    const int old = __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return old;
+}
+__device__ __forceinline__ void lds_publish(int* p, int v) {
+    lds_wait();
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ int lds_peek(const int* p) {
+    const int v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return v;
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // wave64 cross-lane exchange with lane ^ M: DPP within rows of 16 lanes, permlane swaps across rows.
 // Every cross-lane read (DPP, permlane, readlane, ballot) runs in wave-uniform control flow with all 64 lanes
@@ -407,10 +433,12 @@ __device__ __forceinline__ void cnt_add(int id, int tlo, int thi, uint32_t w) {
     }
 }
 
+// Clears the first `words` words of the table (rounded up to 4: segments are multiples of 1024 ids) with threads
+// tid = 0..WG-1.
 template <int WG>
-__device__ __forceinline__ void cnt_zero(int words) {
-    const int n4 = (words + 3) & ~3;  // within the table: segments are multiples of 1024 ids
-    for (int i = 4 * (int) threadIdx.x; i < n4; i += 4 * WG) *reinterpret_cast<uint4*>(s_cnt + i) = make_uint4(0u, 0u, 0u, 0u);
+__device__ __forceinline__ void cnt_zero(int words, int tid = (int) threadIdx.x) {
+    const int n4 = (words + 3) & ~3;
+    for (int i = 4 * tid; i < n4; i += 4 * WG) *reinterpret_cast<uint4*>(s_cnt + i) = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // Where a row's raw history lies: ids [s0, s1) of hist_ids; [b0, b1) is its 16-byte aligned body (empty when the
@@ -422,10 +450,10 @@ struct RawHistory {
 // Counts every history id in [tlo, thi) into the table: the prefetched int4s, the rest of a raw history, a
 // bucketed history, and the extra lists.
 // Without PREF the whole raw history is read from memory (hq unused).
+// The counting threads are tid = 0..WG-1 (the workgroup's threads, or a subset of its waves).
 template <int WG, bool C16, bool PREF>
 __device__ __forceinline__ void count_history(const RowsArgs& a, int row, int tlo, int thi, const int4 (&hq)[HR],
-                                              const RawHistory& rh) {
-    const int tid = threadIdx.x;
+                                              const RawHistory& rh, int tid) {
     if (a.hist_off) {
         if (PREF) {
 #pragma unroll
@@ -703,7 +731,7 @@ __device__ __forceinline__ uint64_t segment_slow(const RowsArgs& a, const float*
             cnt_zero<WG>(whi - wlo);
             __syncthreads();
             const int4 none[HR] = {};
-            count_history<WG, false, false>(a, row, wlo, whi, none, rh);
+            count_history<WG, false, false>(a, row, wlo, whi, none, rh, (int) threadIdx.x);
             __syncthreads();
             scan_exact<NW, false>(w, a, L, wlo, whi, true, wlo, t_row, lane, wave);
         }
@@ -906,6 +934,39 @@ __device__ __forceinline__ CallIn read_call(const RowsArgs& a, int row) {
     return c;
 }
 
+// The row's last workgroup, wave 0 (all lanes), with at most 8 segments: the lists (each sorted, the first k
+// entries valid) are merged as a tree, pairs, then pairs of pairs; every lane loads from every list slot
+// (clamped to the row's lists; entries past k are stale and zeroed), so the loads are issued together. Odd lists
+// are read reversed (ascending); results are merged descending where they are a left operand, ascending where a
+// right one. Then the tail (sampler.cpp:53-88) and the row's token.
+__device__ __forceinline__ void merge_few_tail(const RowsArgs& a, int row, const uint64_t* cand, int k, uint32_t seq,
+                                               int32_t draft, double u_row, int lane) {
+    const uint64_t exp_tab = kExp2Tab[lane & 31];
+    uint64_t lk[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) lk[s] = load_dev(&cand[(int64_t) min(s, a.segs - 1) * KCAP + ((s & 1) ? 63 - lane : lane)]);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) lk[s] = (s < a.segs && ((s & 1) ? 63 - lane : lane) < k) ? lk[s] : 0ull;
+    uint64_t lst = a.segs > 1 ? bitonic_stage<64, true>(max64(lk[0], lk[1]), lane) : lk[0];
+    if (a.segs > 2) {
+        const uint64_t m23 = bitonic_stage<64, false>(max64(lk[2], lk[3]), lane);
+        if (a.segs > 4) {
+            const uint64_t m45 = bitonic_stage<64, true>(max64(lk[4], lk[5]), lane);
+            const uint64_t m67 = bitonic_stage<64, false>(max64(lk[6], lk[7]), lane);
+            const uint64_t m0123 = bitonic_stage<64, true>(max64(lst, m23), lane);
+            const uint64_t m4567 = bitonic_stage<64, false>(max64(m45, m67), lane);
+            lst = bitonic_stage<64, true>(max64(m0123, m4567), lane);
+        } else {
+            lst = bitonic_stage<64, true>(max64(lst, m23), lane);
+        }
+    }
+    const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
+    if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
+    const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
+                                a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
+    if (lane == 0) publish(a, row, tok, seq, draft);
+}
+
 // Loads this thread's logits of groups I0 <= i < I1: ids lb + 4*(i*WG + tid) + e.
 //  * FULL: every group is a whole aligned float4 inside the row, read through the buffer resource `seg` (base =
 //    logit lb) with one offset register for all groups;
@@ -1036,18 +1097,18 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
         // (the barrier comes before the rest of the segment: every wave reaches it having issued few loads; a
         // wave whose loads wait for issue slots would hold the others here)
         __syncthreads();  // table zeroed
-        // Lazy 16-wave rows: waves 4..15, whose loads wait behind the first group's anyway, count before issuing
-        // the middle batch, so that the table is complete (and the early bound can form) sooner.
+        // Lazy 16-wave rows: waves 4..15, whose loads wait behind the first group's anyway, count before
+        // issuing the middle batch, so that the table is complete (and the early bound can form) sooner.
         const bool count_first = late && NW == 16 && wave >= 4;
         if (!count_first) load_groups<FULL, WG, EPT, Q1, Q3>(v, vec, seg_rsrc, L, lb, hi);
         if (!wide) {
-            count_history<WG, C16, true>(a, row, lb, hi, hq, rh);
-            // (before the last batch, for the same reason; late counts are first read after the scan, once every
-            // wave has announced its count: LDS operations of a wave complete in order)
+            count_history<WG, C16, true>(a, row, lb, hi, hq, rh, (int) threadIdx.x);
+            // (before the last batch, for the same reason; late counts are first read after the scan, once
+            // every wave has announced its count: LDS operations of a wave complete in order)
             if (!late) {
                 __syncthreads();  // table complete
             } else {
-                if (lane == 0) __hip_atomic_fetch_add(&s_counted, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (lane == 0) lds_raise(&s_counted, 1);
                 __builtin_amdgcn_sched_barrier(0);  // (the last batch stays after the count)
             }
         }
@@ -1072,14 +1133,14 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             const int mid = min(hi, lb + SEG / 2);
             cnt_zero<WG>(mid - lb);
             __syncthreads();
-            count_history<WG, false, false>(a, row, lb, mid, none, rh);
+            count_history<WG, false, false>(a, row, lb, mid, none, rh, (int) threadIdx.x);
             __syncthreads();
             apply_counts<WG, EPT, false, FULL, 0, NV / 2>(v, lb, hi, lb, a.p);
             if (mid < hi) {
                 __syncthreads();
                 cnt_zero<WG>(hi - mid);
                 __syncthreads();
-                count_history<WG, false, false>(a, row, mid, hi, none, rh);
+                count_history<WG, false, false>(a, row, mid, hi, none, rh, (int) threadIdx.x);
                 __syncthreads();
                 apply_counts<WG, EPT, false, FULL, NV / 2, NV>(v, lb, hi, mid, a.p);
             }
@@ -1149,7 +1210,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             // others do, so the wait ends; the bound on it is a guard only)
             bool counted = false;
             for (int spin = 0; spin < a.spin_limit && !counted; ++spin) {
-                counted = __hip_atomic_load(&s_counted, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW;
+                counted = lds_peek(&s_counted) >= NW;
                 if (!counted) __builtin_amdgcn_s_sleep(1);
             }
             if (!counted && lane == 0) report_fault(a, FAULT_COUNT_WAIT);
@@ -1181,14 +1242,14 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                 const int g = wave >> 2;
                 s_mx<NW>[wave][lane] = sort32<true>(ord_f32(m1), lane);
                 int n = 0;
-                if (lane == 0) n = __hip_atomic_fetch_add(&s_arr[g], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (lane == 0) n = lds_raise(&s_arr[g], 1);
                 if (rdlanei(n, 0) == 3) {
                     gl = s_mx<NW>[4 * g][lane];
 #pragma unroll
                     for (int o = 1; o < 4; ++o) gl = merge32(gl, s_mx<NW>[4 * g + o][63 - lane], lane);
                     s_mx4<NW>[g][lane] = gl;
                     n = 0;
-                    if (lane == 0) n = __hip_atomic_fetch_add(&s_arr[3], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (lane == 0) n = lds_raise(&s_arr[3], 1);
                     if (rdlanei(n, 0) == eg - 1) {
 #pragma unroll
                         for (int o = 0; o < 3; ++o)
@@ -1196,7 +1257,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
                         const uint32_t qw = (uint32_t) rdlanei((int) gl, k - 1);  // all lanes active
                         if (lane == 0) {
                             s_qe = qw;
-                            __hip_atomic_store(&s_qready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                            lds_publish(&s_qready, 1);
                         }
                     }
                 }
@@ -1204,7 +1265,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             // (the bound on the wait is a guard only: if it expires the launch reports a fault)
             bool ready = false;
             for (int spin = 0; spin < a.spin_limit && !ready; ++spin) {
-                ready = __hip_atomic_load(&s_qready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+                ready = lds_peek(&s_qready) != 0;
                 if (!ready) __builtin_amdgcn_s_sleep(1);
             }
             if (!ready && lane == 0) report_fault(a, FAULT_BOUND_WAIT);
@@ -1289,34 +1350,7 @@ __global__ __launch_bounds__(NW * 64) void rows_kernel(RowsArgs a) {
             }
             return;
         }
-        // The lists (each sorted, the first k entries valid) are merged as a tree: pairs, then pairs of pairs.
-        // Every lane loads from every list slot (clamped to the row's lists; entries past k are stale and zeroed),
-        // so the loads are issued together, with the row's uniform. Odd lists are read reversed (ascending).
-        const uint64_t exp_tab = kExp2Tab[lane & 31];
-        uint64_t lk[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) lk[s] = load_dev(&cand[(int64_t) min(s, a.segs - 1) * KCAP + ((s & 1) ? 63 - lane : lane)]);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) lk[s] = (s < a.segs && ((s & 1) ? 63 - lane : lane) < k) ? lk[s] : 0ull;
-        // (merged descending where the result is a left operand, ascending where it is a right one)
-        uint64_t lst = a.segs > 1 ? bitonic_stage<64, true>(max64(lk[0], lk[1]), lane) : lk[0];
-        if (a.segs > 2) {
-            const uint64_t m23 = bitonic_stage<64, false>(max64(lk[2], lk[3]), lane);
-            if (a.segs > 4) {
-                const uint64_t m45 = bitonic_stage<64, true>(max64(lk[4], lk[5]), lane);
-                const uint64_t m67 = bitonic_stage<64, false>(max64(lk[6], lk[7]), lane);
-                const uint64_t m0123 = bitonic_stage<64, true>(max64(lst, m23), lane);
-                const uint64_t m4567 = bitonic_stage<64, false>(max64(m45, m67), lane);
-                lst = bitonic_stage<64, true>(max64(m0123, m4567), lane);
-            } else {
-                lst = bitonic_stage<64, true>(max64(lst, m23), lane);
-            }
-        }
-        const int kk = min(k, (int) __popcll(ballot(lst != 0ull && lane < k)));
-        if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = lane < kk ? lst : 0ull;
-        const int tok = sample_tail(lst, kk, a.p, u_row, exp_tab, lane, a.dbg_probs ? a.dbg_probs + row * KCAP : nullptr,
-                                    a.dbg_meta ? a.dbg_meta + row * 2 : nullptr);
-        if (lane == 0) publish(a, row, tok, seq, draft);
+        merge_few_tail(a, row, cand, k, seq, draft, u_row, lane);
         return;
     }
     __syncthreads();
@@ -1439,7 +1473,7 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
         const int4 none[HR] = {};
         cnt_zero<WIDE_WG>(hi - lo);
         __syncthreads();
-        count_history<WIDE_WG, false, false>(a, row, lo, hi, none, rh);
+        count_history<WIDE_WG, false, false>(a, row, lo, hi, none, rh, (int) threadIdx.x);
         __syncthreads();
     }
     const int ib = w.id_bits;
