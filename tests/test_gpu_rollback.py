@@ -1,7 +1,7 @@
 """GPU parity of the verify step's consumer, the recurrent-state rollback (src/engine.cpp:578-583,
 src/state.cpp:162-184), through the C ABI: kls_rollback_recurrent against the oracle's restatement on synthetic
 state buffers, bit for bit, for every rollback depth s = 0..nb-1 (accepted = nb-1..0), each snapshot type (f32,
-f16, bf16), the vector path (rows multiples of 8, aligned) and the element path (odd rows, padded strides), at a
+f16, bf16), the vector path (rows multiples of 4, 16-byte aligned, with and without padding) and the element path (odd rows, padded strides), at a
 27B-class layout (48 layers, conv rows of 30,720 f32, ssm rows of 786,432), and chained after a real verify step
 on the same stream with the accepted count read from device memory."""
 import ctypes as C
@@ -101,6 +101,7 @@ def rollback(torch, st, d_acc_ptr, nb, stream=None):
 SHAPES = [
     # layers, conv_row, ssm_row, pad (elements of padding in each stride)
     (3, 64, 4096, 0),      # vector path
+    (2, 36, 1004, 4),      # vector path: rows multiples of 4 (not 8), padded 16-byte strides
     (2, 30, 1001, 3),      # element path: odd rows, padded strides
 ]
 
