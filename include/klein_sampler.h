@@ -191,7 +191,7 @@ int kls_recurrent_create(const kls_recurrent_desc* desc, kls_recurrent_handle* o
 int kls_recurrent_destroy(kls_recurrent_handle r);
 
 /* Replaces `rejected = (nb - 1) - accepted; if (rejected > 0) state->rollback_recurrent(gpu, rejected)` of
- * Engine::generate (src/engine.cpp:580-583) with State::rollback_recurrent (src/state.cpp:162-184): for every
+ * Engine::generate (src/engine.cpp:578-582) with State::rollback_recurrent (src/state.cpp:162-184): for every
  * layer, conv slot s is copied over slot 0 and snapshot row s - 1 is converted to f32 into ssm, s = rejected.
  * `accepted` is read from device memory (d_accepted: kls_device_results's, or any device int32) by the kernel,
  * so the call can be enqueued right after kls_verify_enqueue on the same stream, before the host knows the

@@ -64,7 +64,7 @@ __device__ __forceinline__ float snap_elem(const void* p, int64_t i) {
 // instruction of a wave writes 1 KB of consecutive f32 (whole cache lines); else 1 element.
 template <int SNAP, bool VEC>
 __global__ __launch_bounds__(256) void rollback_kernel(RollbackArgs a) {
-    // engine.cpp:580: rejected = (nb - 1) - accepted (clamped: a value outside [0, nb - 1] moves nothing out of
+    // engine.cpp:578: rejected = (nb - 1) - accepted (clamped: a value outside [0, nb - 1] moves nothing out of
     // bounds); state.cpp:163: nothing to do for s <= 0
     const int acc = *a.accepted;
     const int s = (acc >= 0 && acc < a.nb) ? (a.nb - 1) - acc : 0;

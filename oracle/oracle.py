@@ -236,7 +236,7 @@ def snap_to_f32(row: np.ndarray, snap_type: int) -> np.ndarray:
 
 def rollback_recurrent(conv: np.ndarray, ssm: np.ndarray, snap: np.ndarray | None, snap_type: int, accepted: int,
                        nb: int):
-    """One layer of Engine::generate's rollback: rejected = (nb - 1) - accepted (src/engine.cpp:580), then
+    """One layer of Engine::generate's rollback: rejected = (nb - 1) - accepted (src/engine.cpp:578), then
     State::rollback_recurrent(gpu, rejected) (src/state.cpp:162-184): nothing for s <= 0, else conv slot s over
     slot 0 (state.cpp:177) and snapshot row s - 1 converted into ssm (state.cpp:178). conv: [n_snapshots, conv_row]
     f32; ssm: [ssm_row] f32; snap: [n_snapshots - 1, ssm_row] (f32, or uint16 bits of f16 / bf16). Returns the new
