@@ -51,9 +51,12 @@ typedef void* kls_stream;
 
 /* Replaces Sampler::Sampler (src/sampler.cpp:11). Binds the current HIP device, allocates every buffer the
  * handle will use (no allocation happens in the calls below), and starts with an empty token history.
- * max_rows bounds the rows of kls_verify and kls_sample_batch. A top-k above 64 (or no limit) takes a slower
- * path that keys and sorts every logit of a row (2 x 8 bytes per logit per row of device memory); it needs
- * n_vocab * max_rows below 2^32 (KLS_ERR_UNSUPPORTED otherwise). */
+ * max_rows bounds the rows of kls_verify and kls_sample_batch. A top-k of 65 to 1024 takes the mid path: one
+ * kernel, like top-k <= 64, with a 128 KB candidate buffer per row (vocabularies of up to 16384 / top_k segments
+ * of 32768 ids: n_vocab <= 524,288 for every such top-k). A larger top-k (or no limit) takes a slower path
+ * that keys and sorts every logit of a row (2 x 8 bytes per logit per row of device memory, several launches
+ * that a verify step does not capture in a graph); it needs n_vocab * max_rows below 2^32
+ * (KLS_ERR_UNSUPPORTED otherwise). */
 int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* out);
 
 int kls_destroy(kls_handle h);
@@ -233,6 +236,11 @@ int kls_debug_set_layout(kls_handle h, const kls_debug_layout* layout);
  * *out_us = microseconds per kernel. Needs a completed verify step on the handle (KLS_ERR_INVALID_ARG otherwise);
  * the handle's results are those of that step again afterwards. */
 int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, double* out_us);
+
+/* Test hook, no counterpart in the reference: *out_path = the kernel path the handle's sampling calls take
+ * (greedy and top-k <= 64: FAST; top-k 65..1024: MID; larger or no limit: WIDE). */
+enum kls_path { KLS_PATH_FAST = 0, KLS_PATH_MID = 1, KLS_PATH_WIDE = 2 };
+int kls_debug_path(kls_handle h, int32_t* out_path);
 
 /* Test hook, no counterpart in the reference: the wide top-k tail's parallel replay of a sequential double sum
  * (src/sampler.cpp:58,70-77,84-87 accumulate this way) over the n device doubles d_terms from acc0:

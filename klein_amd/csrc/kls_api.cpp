@@ -131,7 +131,10 @@ struct kls_sampler {
     float* d_rows_buf = nullptr;  // host logits are copied here
     int max_segs = 0;
 
-    // wide top-k (k above KCAP): key buffers and the sort's scratch
+    // mid top-k (KCAP < k <= MID_KMAX, one kernel): the rows' candidate buffers
+    bool mid = false;
+    MidArgs m{};
+    // wide top-k (larger k, or no limit): key buffers and the sort's scratch
     bool wide = false;
     WideArgs w{};
 
@@ -284,7 +287,12 @@ RowsArgs base_args(kls_sampler* h, const float* logits, int rows, int64_t stride
     a.row_stride = stride;
     a.V = h->V;
     a.n_rows = rows;
-    segments_for(h, rows, greedy, &a.seg_len, &a.segs);
+    if (h->mid && !greedy) {
+        a.seg_len = MID_SEG;
+        a.segs = mid_segments(h->V);
+    } else {
+        segments_for(h, rows, greedy, &a.seg_len, &a.segs);
+    }
     a.p = h->sp;
     a.bucket_shift = h->bucket_shift;
     a.n_buckets = h->n_buckets;
@@ -325,6 +333,12 @@ RowsArgs step_args(kls_sampler* h, const float* logits, int rows, bool verify) {
         a.out_accepted = h->d_accepted;
     }
     return a;
+}
+
+// The sampling kernel of the handle's path over `a` (the fast path or the mid top-k path: one kernel each).
+hipError_t launch_sampling(const kls_sampler* h, const RowsArgs& a, bool penalize, hipStream_t s) {
+    if (h->mid) return launch_mid(a, h->m, penalize, s);
+    return launch_rows(a, h->greedy, penalize, s);
 }
 
 int check_handle(kls_handle h) {
@@ -401,12 +415,12 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
             hipStream_t cap = nullptr;
             KLS_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
             const hipError_t be = hipStreamBeginCapture(cap, hipStreamCaptureModeRelaxed);
-            const hipError_t le = be == hipSuccess ? launch_rows(a, h->greedy, h->penalize, cap) : hipSuccess;
+            const hipError_t le = be == hipSuccess ? launch_sampling(h, a, h->penalize, cap) : hipSuccess;
             hipGraph_t g = nullptr;
             const hipError_t ce = be == hipSuccess ? hipStreamEndCapture(cap, &g) : hipSuccess;
             (void) hipStreamDestroy(cap);
             if (be != hipSuccess) return fail(KLS_ERR_HIP, "hipStreamBeginCapture", be);
-            if (le != hipSuccess) return fail(KLS_ERR_HIP, "launch_rows (capture)", le);
+            if (le != hipSuccess) return fail(KLS_ERR_HIP, "sampling kernel (capture)", le);
             if (ce != hipSuccess) return fail(KLS_ERR_HIP, "hipStreamEndCapture", ce);
             h->graph = g;
             KLS_HIP(hipGraphInstantiate(&h->gexec, h->graph, nullptr, nullptr, 0));
@@ -419,7 +433,7 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
         KLS_HIP(prepare_graph_stream(h->device, s));
         KLS_HIP(hipGraphLaunch(h->gexec, s));
     } else {
-        KLS_HIP(launch_rows(a, h->greedy, h->penalize, s));
+        KLS_HIP(launch_sampling(h, a, h->penalize, s));
     }
     h->inflight = true;
     h->inflight_stream = s;
@@ -502,7 +516,7 @@ int kls_destroy(kls_handle h) {
     void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_seg_cand,
                    h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_accepted,
                    h->d_step, h->d_dbg_keys, h->d_dbg_probs, h->d_dbg_meta,
-                   h->d_rows_buf, h->w.keys, h->w.sorted, h->w.sort_tmp};
+                   h->d_rows_buf, h->w.keys, h->w.sorted, h->w.sort_tmp, h->m.buf, h->m.fill};
     for (void* p : dev)
         if (p) (void) hipFree(p);
     if (h->h_stage) (void) hipHostFree(h->h_stage);
@@ -519,8 +533,10 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     if (n_vocab <= 0) return fail(KLS_ERR_INVALID_ARG, "n_vocab must be positive");
     if (max_rows < 1) return fail(KLS_ERR_INVALID_ARG, "max_rows must be positive");
     const int k = (params->top_k > 0 && params->top_k < n_vocab) ? params->top_k : n_vocab;
-    // k above KCAP (or no limit) takes the wide path, whose keys hold an id and a row index in 32 bits
-    const bool wide = params->temperature > 0.0f && k > KCAP;
+    // k above KCAP: the mid path up to MID_KMAX (while the rows' buffers hold every segment's share), else the
+    // wide path, whose keys hold an id and a row index in 32 bits
+    const bool mid = params->temperature > 0.0f && mid_fits(n_vocab, k);
+    const bool wide = params->temperature > 0.0f && k > KCAP && !mid;
     int row_bits = 0;
     while ((1ll << row_bits) < (long long) max_rows) ++row_bits;
     if (wide && wide_id_bits(n_vocab) + row_bits > 32)
@@ -536,6 +552,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     h->max_rows = max_rows;
     h->k = k;
     h->greedy = params->temperature <= 0.0f;
+    h->mid = mid;
     h->wide = wide;
     h->penalize = params->presence_penalty != 0.0f || params->frequency_penalty != 0.0f ||
                   params->repetition_penalty != 1.0f;
@@ -554,7 +571,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
         return fail(KLS_ERR_HIP, "library stream", e);
     }
     if ((e = hipEventCreateWithFlags(&h->order_ev, hipEventDisableTiming)) != hipSuccess) return oom("event", e);
-    if ((e = prepare_rows_kernels()) != hipSuccess) {
+    if ((e = prepare_rows_kernels()) != hipSuccess || (mid && (e = prepare_mid_kernels()) != hipSuccess)) {
         kls_destroy(h);
         return fail(KLS_ERR_HIP, "kernel LDS limits", e);
     }
@@ -575,6 +592,12 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     ALLOC(h->d_dbg_probs, sizeof(float) * R * KCAP);
     ALLOC(h->d_dbg_meta, sizeof(int32_t) * R * 2);
     ALLOC(h->d_rows_buf, sizeof(float) * R * n_vocab);
+    if (mid) {
+        h->m.k = k;
+        h->m.cap = MID_ROWCAP / mid_segments(n_vocab);
+        ALLOC(h->m.buf, sizeof(uint64_t) * R * MID_ROWCAP);
+        ALLOC(h->m.fill, sizeof(uint32_t) * R);
+    }
     if (wide) {
         h->w.k = k;
         h->w.id_bits = wide_id_bits(n_vocab);
@@ -605,6 +628,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     if ((e = hipMemsetAsync(h->d_hist_boff, 0, sizeof(int32_t) * (h->n_buckets + 1), h->stream)) != hipSuccess)
         return oom("init", e);
     if ((e = hipMemsetAsync(h->d_step, 0, sizeof(uint64_t), h->stream)) != hipSuccess) return oom("init", e);
+    if (mid && (e = hipMemsetAsync(h->m.fill, 0, sizeof(uint32_t) * R, h->stream)) != hipSuccess) return oom("init", e);
     if ((e = hipMemsetAsync(h->d_accepted, 0, sizeof(int32_t), h->stream)) != hipSuccess) return oom("init", e);
     if ((e = hipStreamSynchronize(h->stream)) != hipSuccess) return oom("init", e);
     *out = h;
@@ -736,7 +760,7 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
     if (h->wide)
         KLS_HIP(launch_wide(a, h->w, pen, s));
     else
-        KLS_HIP(launch_rows(a, h->greedy, pen, s));
+        KLS_HIP(launch_sampling(h, a, pen, s));
     return KLS_OK;
 }
 
@@ -829,11 +853,11 @@ int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, doub
     hipStream_t cap = nullptr;
     KLS_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
     hipError_t e = hipStreamBeginCapture(cap, hipStreamCaptureModeRelaxed);
-    for (int i = 0; i < n && e == hipSuccess; ++i) e = launch_rows(h->g_args, h->greedy, h->penalize, cap);
+    for (int i = 0; i < n && e == hipSuccess; ++i) e = launch_sampling(h, h->g_args, h->penalize, cap);
     hipGraph_t g = nullptr;
     const hipError_t ce = hipStreamEndCapture(cap, &g);
     (void) hipStreamDestroy(cap);
-    if (e != hipSuccess) return fail(KLS_ERR_HIP, "launch_rows (capture)", e);
+    if (e != hipSuccess) return fail(KLS_ERR_HIP, "sampling kernel (capture)", e);
     if (ce != hipSuccess) return fail(KLS_ERR_HIP, "hipStreamEndCapture", ce);
     hipGraphExec_t x = nullptr;
     e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
@@ -856,6 +880,13 @@ int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, doub
     if (e != hipSuccess) return fail(KLS_ERR_HIP, "timed replay", e);
     *out_us = (double) ms * 1e3 / ((double) n * reps);
     return check_fault(h);
+}
+
+int kls_debug_path(kls_handle h, int32_t* out_path) {
+    if (int st = check_handle(h)) return st;
+    if (!out_path) return fail(KLS_ERR_INVALID_ARG, "null argument");
+    *out_path = h->wide ? KLS_PATH_WIDE : h->mid ? KLS_PATH_MID : KLS_PATH_FAST;
+    return KLS_OK;
 }
 
 int kls_debug_sum_replay(const double* d_terms, int n, double acc0, int mode, double thr, double* d_out,

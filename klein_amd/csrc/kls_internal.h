@@ -47,6 +47,7 @@ struct ResultBlock {
 // Fault codes (ResultBlock::fault).
 constexpr uint32_t FAULT_COUNT_WAIT = 1;   // the history count table was not announced complete in time
 constexpr uint32_t FAULT_BOUND_WAIT = 2;   // the early bound of a 16-wave segment was not published in time
+constexpr uint32_t FAULT_NARROW = 3;       // a mid top-k threshold bisection did not end (not reachable)
 
 struct SamplingParams {
     float temperature;
@@ -133,6 +134,23 @@ struct WideArgs {
     int32_t id_bits;      // ids are below 1 << id_bits
 };
 
+// Mid top-k (KCAP < k <= MID_KMAX; src/sampler.cpp:42-51), one kernel: 1024-thread workgroups over segments of
+// MID_SEG ids append the logits at or above a per-segment bound (every one of the segment's top-k among them) to
+// the row's buffer of MID_ROWCAP keys (fast-path keys: value image << 32 | ~id); the row's last workgroup selects
+// and sorts the row's top-k from it in LDS and runs the wide path's exact tail.
+constexpr int MID_KMAX = 1024;
+constexpr int MID_SEG = 32768;
+constexpr int MID_ROWCAP = 16384;
+struct MidArgs {
+    uint64_t* buf;    // [n_rows][MID_ROWCAP]
+    uint32_t* fill;   // [n_rows] keys appended so far (left zero)
+    int32_t k;        // KCAP < k <= MID_KMAX
+    int32_t cap;      // keys a segment may append: MID_ROWCAP / segments, at least k
+};
+// Segments of the mid path for V ids, and whether top-k k fits it.
+inline int mid_segments(int V) { return (V + MID_SEG - 1) / MID_SEG; }
+inline bool mid_fits(int V, int k) { return k > KCAP && k <= MID_KMAX && k <= MID_ROWCAP / mid_segments(V); }
+
 // Per-token perplexity / KL-divergence scores (src/main.cpp:308-327; kls_ppl.hip). Row r of logits at
 // logits + r*row_stride, of base log-probabilities (optional) at base + r*base_stride; outputs per row, each
 // optional. Scratch: per (row, segment) a KCAP-word record; per row a ticket counter (left zero).
@@ -183,6 +201,10 @@ hipError_t launch_sum_replay(const double* t, int n, double acc0, int mode, doub
 // launch_rows does).
 hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipStream_t s);
 int wide_id_bits(int V);  // key bits the ids of a V-entry vocabulary take
+// Mid top-k: one kernel over a.n_rows rows of a.segs = mid_segments(V) segments (tokens published as launch_rows
+// does).
+hipError_t launch_mid(const RowsArgs& a, const MidArgs& m, bool penalize, hipStream_t s);
+hipError_t prepare_mid_kernels();  // once per device: LDS limit of the kernel with a count table
 
 // Descending device-wide sort of n 64-bit keys on bits [0, end_bit) (kls_sort.hip). With tmp == nullptr, sets
 // *bytes to the scratch size.

@@ -1490,12 +1490,7 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
     }
 }
 
-// The tail of src/sampler.cpp:53-88 over a row's sorted keys (one workgroup per row): candidate i is the row's
-// i-th key (value descending, id ascending), numbers only (NaN keys sort last and are left out). The per-candidate
-// terms (e_i, then p_i) are computed by every thread into the row's part of the key buffer (free after the
-// sort) as doubles; every sum is then the reference's sequential double chain, one addition per candidate in
-// candidate order, run by wave 0 over 64-candidate chunks (lane j holding candidate c + j) with the loads of the
-// next chunks in flight.
+// The tail over sorted candidates (sorted_tail below) runs on one workgroup of TAIL_WG threads per row.
 constexpr int TAIL_WG = 1024;
 __shared__ int s_wide_n;  // kk, then the min-p length
 
@@ -1661,19 +1656,31 @@ __global__ __launch_bounds__(TAIL_WG) void sum_replay_kernel(const double* t, in
     }
 }
 
-__global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs w) {
-    const int row = (int) blockIdx.x, tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
-    const int ib = w.id_bits, k = w.k;
-    const uint64_t vmask = (1ull << (32 + ib)) - 1ull;
-    const uint32_t idm = (1u << ib) - 1u;
-    const uint64_t* __restrict__ K = w.sorted + (int64_t) row * a.V;
-    double* __restrict__ t = reinterpret_cast<double*>(w.keys + (int64_t) row * a.V);  // per-candidate terms
+// Key layouts the tail reads: the wide path's packed keys, and the fast path's (value image << 32 | ~id).
+struct WideKeyFmt {
+    int ib;          // id bits
+    uint64_t vmask;  // value and id fields
+    uint32_t idm;    // id field
+    __device__ uint32_t img(uint64_t k) const { return (uint32_t) ((k & vmask) >> ib); }
+    __device__ int id(uint64_t k) const { return (int) (~(uint32_t) k & idm); }
+};
+struct FastKeyFmt {
+    __device__ uint32_t img(uint64_t k) const { return (uint32_t) (k >> 32); }
+    __device__ int id(uint64_t k) const { return (int) ~(uint32_t) k; }
+};
+
+// The tail of src/sampler.cpp:53-88 over a row's sorted keys K (value descending, id ascending; the first k are
+// the candidates, ended early by the first key of value image 0, a NaN), with the whole workgroup (TAIL_WG
+// threads, uniform control flow): the per-candidate terms (e_i, then p_i) go to t[0..k) as doubles, and every sum
+// is the reference's sequential double chain replayed exactly (replay_sum). Publishes the row's token.
+template <typename Fmt>
+__device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k, double* t, const CallIn& cin,
+                            const Fmt& fmt) {
+    const int tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
     const SamplingParams p = a.p;
-    const CallIn cin = read_call<false>(a, row);
     const uint32_t seq = cin.seq;
     const int32_t draft = cin.draft;
-    auto img = [&](int i) { return (uint32_t) ((K[i] & vmask) >> ib); };  // value image, 0: NaN
-    const uint32_t o0 = img(0);
+    const uint32_t o0 = k > 0 ? fmt.img(K[0]) : 0u;
     if (o0 == 0u) {  // no number in the row: the fast path's empty candidate list
         if (wave == 0) {
             if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = 0ull;
@@ -1692,7 +1699,7 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
     if (tid == 0) s_wide_n = k;
     __syncthreads();
     for (int i = tid; i < k; i += TAIL_WG) {
-        const uint32_t o = img(i);
+        const uint32_t o = fmt.img(K[i]);
         if (o == 0u) atomicMin(&s_wide_n, i);
         t[i] = (double) expf_glibc(__fdiv_rn(__fsub_rn(unord_f32(o), maxl), p.temperature));
     }
@@ -1734,9 +1741,9 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
     replay_sum(t, n, r0, [](double r, int) { return r <= 0.0; }, &st);
     const int idx = st >= 0 ? st : n - 1;
     if (wave != 0) return;
-    const int tok = (int) (~(uint32_t) K[idx] & idm);
-    const uint32_t ol = act ? img(lane) : 0u;
-    if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = act ? ((uint64_t) ol << 32) | (uint64_t) ~(~(uint32_t) K[lane] & idm) : 0ull;
+    const int tok = fmt.id(K[idx]);
+    const uint64_t kl = act ? K[lane] : 0ull;
+    if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = act ? ((uint64_t) fmt.img(kl) << 32) | (uint64_t) ~(uint32_t) fmt.id(kl) : 0ull;
     if (a.dbg_probs) a.dbg_probs[row * KCAP + lane] = dbg_p;
     if (lane == 0) {
         if (a.dbg_meta) {
@@ -1745,6 +1752,343 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
         }
         publish(a, row, tok, seq, draft);
     }
+}
+
+// The wide path's tail: one workgroup per row over the row's part of the sorted key buffer, the terms in the
+// row's part of the (free after the sort) unsorted one.
+__global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs w) {
+    const int row = (int) blockIdx.x;
+    const WideKeyFmt fmt{w.id_bits, (1ull << (32 + w.id_bits)) - 1ull, (1u << w.id_bits) - 1u};
+    const CallIn cin = read_call<false>(a, row);
+    sorted_tail(a, row, w.sorted + (int64_t) row * a.V, w.k, reinterpret_cast<double*>(w.keys + (int64_t) row * a.V),
+                cin, fmt);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Mid top-k (KCAP < k <= MID_KMAX; src/sampler.cpp:42-51) in one launch. Workgroup = (row, segment of MID_SEG
+// ids), 16 waves, 32 logits per thread held in registers:
+//   1. the history counts are applied to every logit (a 32-bit LDS table over the segment);
+//   2. a bound reached by at least ks = min(k, segment length) logits of the segment: each wave takes the
+//      ceil(ks/16)-th largest of its lanes' two largest values (128 distinct logits), and the smallest of the 16
+//      waves' values has at least 16 * ceil(ks/16) >= ks logits at or above it, so the segment's top ks are all
+//      at or above it (with fewer numbers than that the bound is 0 and every number qualifies);
+//   3. with more than m.cap keys at or above it (ties at the bound), the key threshold is bisected until between
+//      ks and m.cap keys reach it (keys are distinct, so such a threshold exists);
+//   4. the keys that reach it are appended to the row's buffer (space taken with a device-scope counter), so the
+//      buffer holds every key of the row's top k;
+//   5. the row's last workgroup (ticket) holds the buffer in registers (16 keys per thread), forms the same
+//      bound for k over it (bisected down to MID_SORT keys if needed), sorts the keys that reach it in LDS and
+//      runs sorted_tail over the first k.
+// Counters are left zero for the next launch (the ticket by publish, the buffer's counter by the last workgroup).
+constexpr int MID_NW = 16, MID_WG = MID_NW * 64, MID_EPT = 32, MID_RK = MID_ROWCAP / MID_WG;
+constexpr int MID_SORT = 4096;  // keys the row's sort holds
+static_assert(MID_WG * MID_EPT == MID_SEG, "segment length");
+static_assert(MID_WG == TAIL_WG, "the row's tail runs on the mid workgroup");
+static_assert(MID_KMAX <= MID_NW * 64, "a wave's bound index is at most 64");
+static_assert(MID_SORT == 4 * MID_WG && MID_SORT >= MID_KMAX, "the sort's layout");
+
+__shared__ uint32_t s_mid_w[MID_NW];  // per-wave bounds
+__shared__ int s_mid_c[2][MID_NW];    // per-wave counts (two sets, used alternately)
+__shared__ int s_mid_base;
+
+// The j-th largest (1 <= j <= 64) of the 128 values m1, m2 of the wave's lanes (value images, m2 <= m1 in each
+// lane); 0 when fewer than j are nonzero.
+__device__ __forceinline__ uint32_t wave_top2_kth(uint32_t m1, uint32_t m2, int j, int lane) {
+    const uint32_t a = sort32<true>(m1, lane);
+    const uint32_t b = sort32<false>(m2, lane);
+    const uint32_t c = merge32(a, b, lane);  // the top 64 of the union, descending
+    return (uint32_t) rdlanei((int) c, j - 1);
+}
+
+// Workgroup sum of c (every thread calls it). `par` alternates the LDS slots, so one barrier per call suffices:
+// a thread writes a slot again only after a later call's barrier, which every thread passes after its reads.
+__device__ __forceinline__ int mid_sum(int c, int lane, int wave, int& par) {
+    int x = c;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
+    if (lane == 0) s_mid_c[par][wave] = x;
+    __syncthreads();
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < MID_NW; ++w) tot += s_mid_c[par][w];
+    par ^= 1;
+    return tot;
+}
+
+// Exclusive prefix of c over the workgroup's threads (thread order), and the total.
+__device__ __forceinline__ int mid_prefix(int c, int lane, int wave, int& par, int* total) {
+    int x = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        x += lane >= d ? y : 0;
+    }
+    if (lane == 63) s_mid_c[par][wave] = x;
+    __syncthreads();
+    int tot = 0, before = 0;
+#pragma unroll
+    for (int w = 0; w < MID_NW; ++w) {
+        const int sw = s_mid_c[par][w];
+        tot += sw;
+        before += w < wave ? sw : 0;
+    }
+    par ^= 1;
+    *total = tot;
+    return before + x - c;
+}
+
+// A key threshold reached by between `need` and `cap` keys of the workgroup (1 <= need <= cap), given `lo`, one
+// reached by more than cap: bisection over (lo, 2^64 - 2] with workgroup counts, cnt(t) = this thread's keys
+// >= t. Invariants: more than cap keys reach lo, fewer than need reach hi + 1; distinct keys make the count
+// fall by at most one per step of t, so the interval never closes before a threshold is found, and halving a
+// 64-bit interval finds it within 64 rounds. Past that (not reachable) the launch reports a fault and the
+// threshold lets nothing through.
+template <typename F>
+__device__ __forceinline__ uint64_t mid_narrow(const RowsArgs& a, F cnt, uint64_t lo, int need, int cap, int lane,
+                                               int wave, int& par) {
+    uint64_t hi = ~0ull - 1ull;  // no key reaches 2^64 - 1 (the largest value image is that of +inf)
+    for (int it = 0; it < 66; ++it) {
+        const uint64_t mid = lo + (hi - lo) / 2 + 1;
+        const int c = mid_sum(cnt(mid), lane, wave, par);
+        if (c > cap)
+            lo = mid;
+        else if (c < need)
+            hi = mid - 1;
+        else
+            return mid;
+    }
+    if (threadIdx.x == 0) report_fault(a, FAULT_NARROW);
+    return ~0ull;
+}
+
+// Sorts S[0..P) descending with the workgroup (P a power of two in [64, MID_SORT]; U: LDS of the same size for
+// the exchanges). Element i lives in lane i % 64 of wave (i / 64) % 16, register i / 1024: strides below 64 are
+// bitonic steps across lanes, strides of 1024 and 2048 compare a thread's own registers, and strides 64..512 go
+// through LDS, the two buffers alternating so that each such step needs one barrier. Returns the buffer that
+// holds the result (after a barrier).
+__device__ __forceinline__ uint64_t* mid_sort(uint64_t* S, uint64_t* U, int P, int lane, int wave) {
+    constexpr int R = MID_SORT / MID_WG;
+    const int nch = P >> 6;  // chunks of 64
+    uint64_t x[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int c = r * MID_NW + wave;
+        x[r] = c < nch ? S[c * 64 + lane] : 0ull;
+        // chunks alternately descending and ascending: every block of 128 is then bitonic
+        if (c < nch) x[r] = (c & 1) ? sort64<false>(x[r], lane) : sort64<true>(x[r], lane);
+    }
+    uint64_t* bufs[2] = {U, S};
+    int nb = 0;
+    for (int size = 128; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride >= 64; stride >>= 1) {
+            if (stride >= MID_WG) {
+                const int rs = stride / MID_WG;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int c = r * MID_NW + wave;
+                    if ((r & rs) == 0 && c < nch) {
+                        const int r2 = r | rs;
+                        const bool desc = ((c * 64) & size) == 0;
+                        const uint64_t mx = max64(x[r], x[r2]), mn = min64(x[r], x[r2]);
+                        x[r] = desc ? mx : mn;
+                        x[r2] = desc ? mn : mx;
+                    }
+                }
+            } else {
+                uint64_t* B = bufs[nb];
+                nb ^= 1;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int c = r * MID_NW + wave;
+                    if (c < nch) B[c * 64 + lane] = x[r];
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int c = r * MID_NW + wave;
+                    if (c < nch) {
+                        const int i = c * 64 + lane;
+                        const uint64_t y = B[i ^ stride];
+                        const bool lower = (i & stride) == 0, desc = (i & size) == 0;
+                        x[r] = (lower == desc) ? max64(x[r], y) : min64(x[r], y);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int c = r * MID_NW + wave;
+            if (c < nch) x[r] = ((c * 64) & size) == 0 ? bitonic_stage<64, true>(x[r], lane) : bitonic_stage<64, false>(x[r], lane);
+        }
+    }
+    uint64_t* out = bufs[nb];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int c = r * MID_NW + wave;
+        if (c < nch) out[c * 64 + lane] = x[r];
+    }
+    __syncthreads();
+    return out;
+}
+
+template <bool PENALIZE>
+__global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
+    constexpr int WG = MID_WG, EPT = MID_EPT, NV = EPT / 4;
+    const int tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const int segs = a.segs;
+    const int row = (int) blockIdx.x / segs, seg = (int) blockIdx.x - row * segs;
+    const int lo = seg * MID_SEG, hi = min(a.V, lo + MID_SEG);
+    const float* __restrict__ L = a.logits + (int64_t) row * a.row_stride;
+    const bool vec = (reinterpret_cast<uintptr_t>(L) & 15u) == 0;
+    // logit (i, e) of this thread: id lo + 4*(i*WG + tid) + e; NaN past the segment (never a candidate)
+    float v[EPT];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int b = lo + 4 * (i * WG + tid);
+        if (vec && b + 3 < hi) {
+            const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(L + b));
+            v[4 * i + 0] = f[0];
+            v[4 * i + 1] = f[1];
+            v[4 * i + 2] = f[2];
+            v[4 * i + 3] = f[3];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * i + e] = b + e < hi ? L[b + e] : __uint_as_float(0x7fc00000u);
+        }
+    }
+    if (PENALIZE) {
+        RawHistory rh;
+        if (a.hist_off) {
+            rh.s0 = max(a.hist_off[row], 0);
+            rh.s1 = max(a.hist_off[row + 1], rh.s0);
+            const bool hv = (reinterpret_cast<uintptr_t>(a.hist_ids) & 15u) == 0;
+            rh.b0 = hv ? min(rh.s1, (rh.s0 + 3) & ~3) : rh.s1;
+            rh.b1 = hv ? max(rh.b0, rh.s1 & ~3) : rh.s1;
+        }
+        const int4 none[HR] = {};
+        cnt_zero<WG>(hi - lo, tid);
+        __syncthreads();
+        count_history<WG, false, false>(a, row, lo, hi, none, rh, tid);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int id = lo + 4 * (i * WG + tid) + e;
+                if (id < hi) {
+                    const uint32_t c = s_cnt[id - lo];
+                    if (c != 0u) v[4 * i + e] = penalize(v[4 * i + e], c, a.p);
+                }
+            }
+        }
+    }
+    int par = 0;
+    const int ks = min(m.k, hi - lo);
+    uint32_t m1 = 0u, m2 = 0u;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const uint32_t o = ord_f32(v[j]);
+        m2 = max(m2, min(m1, o));
+        m1 = max(m1, o);
+    }
+    const uint32_t tw = wave_top2_kth(m1, m2, (ks + MID_NW - 1) / MID_NW, lane);
+    if (lane == 0) s_mid_w[wave] = tw;
+    __syncthreads();
+    uint32_t bnd = 0xffffffffu;
+#pragma unroll
+    for (int w = 0; w < MID_NW; ++w) bnd = min(bnd, s_mid_w[w]);
+    uint64_t T = (uint64_t) max(bnd, 1u) << 32;  // (numbers only: NaN keys are below 2^32)
+    auto cnt = [&](uint64_t t) {
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) c += mk_key(v[4 * i + e], lo + 4 * (i * WG + tid) + e) >= t ? 1 : 0;
+        }
+        return c;
+    };
+    int total;
+    int off = mid_prefix(cnt(T), lane, wave, par, &total);
+    if (total > m.cap) {
+        T = mid_narrow(a, cnt, T, ks, m.cap, lane, wave, par);
+        off = mid_prefix(cnt(T), lane, wave, par, &total);
+    }
+    if (tid == 0) s_mid_base = (int) atomicAdd(&m.fill[row], (uint32_t) total);
+    __syncthreads();
+    uint64_t* const buf = m.buf + (int64_t) row * MID_ROWCAP;
+    int o = s_mid_base + off;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint64_t key = mk_key(v[4 * i + e], lo + 4 * (i * WG + tid) + e);
+            if (key >= T) {
+                if (o < MID_ROWCAP) store_dev(&buf[o], key);
+                ++o;
+            }
+        }
+    }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&a.row_ticket[row], 1u) == (uint32_t) (segs - 1);
+    __syncthreads();
+    if (!s_last) return;
+
+    // ---- the row's last workgroup
+    const CallIn cin = read_call<false>(a, row);
+    if (tid == 0)
+        s_mid_base = (int) __hip_atomic_exchange(&m.fill[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int N = min(s_mid_base, MID_ROWCAP);
+    const int k = m.k;
+    uint64_t rk[MID_RK];
+#pragma unroll
+    for (int r = 0; r < MID_RK; ++r) {
+        const int g = tid + r * WG;
+        rk[r] = g < N ? load_dev(&buf[g]) : 0ull;
+    }
+    auto cnt2 = [&](uint64_t t) {
+        int c = 0;
+#pragma unroll
+        for (int r = 0; r < MID_RK; ++r) c += rk[r] >= t ? 1 : 0;
+        return c;
+    };
+    uint64_t T2 = 1ull;  // (every buffered key: all are numbers)
+    if (N > MID_SORT) {
+        uint32_t q1 = 0u, q2 = 0u;
+#pragma unroll
+        for (int r = 0; r < MID_RK; ++r) {
+            const uint32_t ov = (uint32_t) (rk[r] >> 32);
+            q2 = max(q2, min(q1, ov));
+            q1 = max(q1, ov);
+        }
+        const uint32_t tw2 = wave_top2_kth(q1, q2, (k + MID_NW - 1) / MID_NW, lane);
+        if (lane == 0) s_mid_w[wave] = tw2;
+        __syncthreads();
+        uint32_t b2 = 0xffffffffu;
+#pragma unroll
+        for (int w = 0; w < MID_NW; ++w) b2 = min(b2, s_mid_w[w]);
+        T2 = (uint64_t) max(b2, 1u) << 32;
+        if (mid_sum(cnt2(T2), lane, wave, par) > MID_SORT) T2 = mid_narrow(a, cnt2, T2, k, MID_SORT, lane, wave, par);
+    }
+    int n2;
+    int o2 = mid_prefix(cnt2(T2), lane, wave, par, &n2);
+    n2 = min(n2, MID_SORT);
+    uint64_t* const S = reinterpret_cast<uint64_t*>(s_cnt);  // (the count table is no longer needed)
+    uint64_t* const U = S + MID_SORT;
+    int P = 64;
+    while (P < n2) P <<= 1;
+    for (int i = n2 + tid; i < P; i += WG) S[i] = 0ull;
+#pragma unroll
+    for (int r = 0; r < MID_RK; ++r) {
+        if (rk[r] >= T2) {
+            if (o2 < MID_SORT) S[o2] = rk[r];
+            ++o2;
+        }
+    }
+    __syncthreads();
+    uint64_t* const K = mid_sort(S, U, P, lane, wave);
+    sorted_tail(a, row, K, min(k, n2), reinterpret_cast<double*>(K == S ? U : S), cin, FastKeyFmt{});
 }
 
 // LDS of the history count table: 4 bytes per id for 4-wave workgroups, 2 for 16-wave ones.
@@ -1839,6 +2183,27 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(TAIL_WG), 0, s, a, w);
     return hipGetLastError();
+}
+
+hipError_t launch_mid(const RowsArgs& a, const MidArgs& m, bool penalize, hipStream_t s) {
+    if (m.k <= KCAP || m.k > MID_KMAX || a.segs != mid_segments(a.V) || m.cap < m.k ||
+        (int64_t) m.cap * a.segs > MID_ROWCAP)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned) (a.n_rows * a.segs));
+    if (penalize)
+        hipLaunchKernelGGL(mid_kernel<true>, grid, dim3(MID_WG), MID_SEG * sizeof(uint32_t), s, a, m);
+    else
+        hipLaunchKernelGGL(mid_kernel<false>, grid, dim3(MID_WG), 2 * MID_SORT * sizeof(uint64_t), s, a, m);
+    return hipGetLastError();
+}
+
+hipError_t prepare_mid_kernels() {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mid_kernel<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int) (MID_SEG * sizeof(uint32_t)));
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mid_kernel<false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * MID_SORT * sizeof(uint64_t)));
+    return e;
 }
 
 hipError_t launch_sum_replay(const double* t, int n, double acc0, int mode, double thr, double* out, hipStream_t s) {

@@ -87,6 +87,13 @@ class Sampler:
         """Raises if a kernel of this handle gave up an internal wait since the last check (kls_check)."""
         _lib.check(_lib.lib().kls_check(self._h), "kls_check")
 
+    @property
+    def path(self) -> str:
+        """The kernel path of the handle's sampling calls: "fast", "mid" or "wide" (kls_debug_path)."""
+        v = C.c_int32()
+        _lib.check(_lib.lib().kls_debug_path(self._h, C.byref(v)), "kls_debug_path")
+        return {_lib.KLS_PATH_FAST: "fast", _lib.KLS_PATH_MID: "mid", _lib.KLS_PATH_WIDE: "wide"}[v.value]
+
     def close(self):
         if self._h is not None:
             _lib.lib().kls_destroy(self._h)

@@ -1,7 +1,9 @@
-"""GPU parity of the wide top-k path (top_k above 64, or no limit: src/sampler.cpp:42-51 with k up to V): every
-logit keyed and sorted on the device, then the reference's tail over the sorted candidates. Token ids, the first
-64 candidates (ids and probabilities), the candidate count and the kept count bit-exact against the oracle, with
-and without penalties, through the batch entry point, single-row sampling and the verify step."""
+"""GPU parity of top-k above 64 (src/sampler.cpp:42-51 with k up to V): the mid path (k up to 1024: candidates
+above per-segment bounds, selected and sorted per row in one kernel) and the wide path (larger k or no limit:
+every logit keyed and sorted on the device), each followed by the reference's tail over the sorted candidates.
+Token ids, the first 64 candidates (ids and probabilities), the candidate count and the kept count bit-exact
+against the oracle, with and without penalties, through the batch entry point, single-row sampling and the
+verify step; each case asserts the path it runs on."""
 import numpy as np
 import pytest
 
@@ -44,6 +46,13 @@ def head_rows(rng, rows, V, scale=1.5):
 def zipf_history(rng, V, n):
     ranks = np.minimum(rng.zipf(1.1, n), V) - 1
     return rng.permutation(V)[ranks].astype(np.int32)
+
+
+def expected_path(V, k):
+    """The path kls_create picks: mid for 64 < k <= 1024 while 16384 / segments (of 32768 ids) >= k."""
+    k = k if 0 < k < V else V
+    segs = (V + 32767) // 32768
+    return "mid" if 64 < k <= 1024 and k <= 16384 // segs else "wide"
 
 
 def check_row(S, O, x, p, u, counts, r, label):
@@ -92,8 +101,9 @@ def test_wide_batch(torch_cuda, K, oracle_lib, case):
     u = rng.random(rows)
     u[0] = 0.9999999
     S = K.Sampler(p, n_vocab=V, max_rows=rows)
+    assert S.path == expected_path(V, k), (case, S.path)
     out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
-    say("wide batch", case, "V", V, "k", k, "rows", rows)
+    say("wide batch", case, "V", V, "k", k, "rows", rows, S.path)
     if pen:
         S.sample_batch(dev(torch, x), dev(torch, u), out, dev(torch, off), dev(torch, ids))
     else:
@@ -118,6 +128,7 @@ def test_wide_ties_and_infinities(torch_cuda, K, oracle_lib):
     p = W.Params(temperature=1.0, top_k=0, top_p=0.5, min_p=0.0)
     u = np.array([0.3, 0.9999, 0.5])
     S = K.Sampler(p, n_vocab=V, max_rows=3)
+    assert S.path == "wide"
     out = torch.full((3,), -1, dtype=torch.int32, device="cuda")
     say("wide ties")
     S.sample_batch(dev(torch, x), dev(torch, u), out)
@@ -129,15 +140,17 @@ def test_wide_ties_and_infinities(torch_cuda, K, oracle_lib):
     S.close()
 
 
-def test_wide_sample_and_verify_with_history(torch_cuda, K, oracle_lib):
-    """The handle's own history (accepted tokens counted on the device) with k above 64: single-row samples,
-    then verify steps with drafts."""
+@pytest.mark.parametrize("k", [500, 2000])
+def test_wide_sample_and_verify_with_history(torch_cuda, K, oracle_lib, k):
+    """The handle's own history (accepted tokens counted on the device) with k above 64 (500: the mid path,
+    2000: the wide one): single-row samples, then verify steps with drafts."""
     O = oracle_lib
     V = 70001
     rng = np.random.default_rng(77)
-    p = W.Params(temperature=0.9, top_k=500, top_p=0.9, min_p=0.02, presence_penalty=0.4, frequency_penalty=0.1,
+    p = W.Params(temperature=0.9, top_k=k, top_p=0.9, min_p=0.02, presence_penalty=0.4, frequency_penalty=0.1,
                  repetition_penalty=1.15, seed=3)
     S = K.Sampler(p, n_vocab=V, max_rows=4)
+    assert S.path == expected_path(V, k)
     counts = np.zeros(V, np.int32)
     for t in rng.integers(0, V, 300):
         S.accept(int(t))
