@@ -198,6 +198,80 @@ def next_rows(torch, klein_amd, W):
     return res
 
 
+def topk_above_64(torch, klein_amd, W):
+    """Top-k above 64 (src/sampler.cpp:42-51 with larger k), which no headline config uses: the verify step's
+    workload with k = 256 and 1,024 on the mid path (one kernel, captured in the step's graph), the 64-row batch
+    at k = 256, and a row without a limit on the wide path (keys, a device-wide sort, the tail: several launches).
+    Every timed call is checked against its first (untimed) result."""
+    import numpy as np
+    from klein_amd import _lib
+    L = _lib.lib()
+    I32P, F64P = C.POINTER(C.c_int32), C.POINTER(C.c_double)
+    v = W.verify()
+    d = torch.from_numpy(v.logits).cuda()
+    dptr = C.c_void_p(d.data_ptr())
+    drafts = np.ascontiguousarray(v.drafts, dtype=np.int32)
+    u = np.ascontiguousarray(v.u, dtype=np.float64)
+    res = {}
+    for k in (256, 1024):
+        S = klein_amd.Sampler(W.Params(temperature=0.6, top_k=k, top_p=0.95), n_vocab=V, max_rows=4)
+        assert S.path == "mid"
+        h, sp = S._h, None
+        t0, a0 = np.zeros(4, np.int32), C.c_int32()
+        _lib.check(L.kls_verify(h, dptr, 4, drafts.ctypes.data_as(I32P), u.ctypes.data_as(F64P),
+                                t0.ctypes.data_as(I32P), C.byref(a0), sp), "kls_verify")
+        tk, ac = np.zeros(4, np.int32), C.c_int32()
+        lat = []
+        for i in range(300):
+            x0 = time.perf_counter_ns()
+            st = L.kls_verify(h, dptr, 4, drafts.ctypes.data_as(I32P), u.ctypes.data_as(F64P),
+                              tk.ctypes.data_as(I32P), C.byref(ac), sp)
+            lat.append((time.perf_counter_ns() - x0) / 1e3)
+            if st:
+                _lib.check(st, "kls_verify")
+            assert ac.value == a0.value and list(tk[:ac.value + 1]) == list(t0[:a0.value + 1]), "mid verify step"
+        kus = C.c_double()
+        _lib.check(L.kls_debug_time_verify(h, 50, 5, sp, C.byref(kus)), "kls_debug_time_verify")
+        res[f"verify_step_k{k}"] = {"path": "mid", "median_us": round(pct(lat, 50), 2),
+                                    "p99_us": round(pct(lat, 99), 2), "kernel_us": round(kus.value, 2)}
+        S.close()
+    # 64 rows at k = 256, no penalties
+    wb = W.batched()
+    SB = klein_amd.Sampler(W.Params(temperature=1.0, top_k=256, top_p=0.9), n_vocab=V, max_rows=64)
+    xb = torch.from_numpy(wb.logits).cuda()
+    ub = torch.from_numpy(wb.u).cuda()
+    ob = torch.full((64,), -1, dtype=torch.int32, device="cuda")
+    first = torch.full((64,), -2, dtype=torch.int32, device="cuda")
+    pb = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+    _lib.check(L.kls_sample_batch(SB._h, pb(xb), 64, V, None, None, pb(ub), pb(first), None), "kls_sample_batch")
+    us_b = graph_us(torch, lambda s: _lib.check(L.kls_sample_batch(SB._h, pb(xb), 64, V, None, None, pb(ub), pb(ob),
+                                                                   s), "kls_sample_batch"), 20)
+    torch.cuda.synchronize()
+    assert torch.equal(ob, first), "mid batch"
+    res["batch_64_rows_k256"] = {"path": "mid", "us_hot": round(us_b, 2),
+                                 "GBps": round(64 * V * 4 / (us_b * 1e-6) / 1e9, 1)}
+    SB.close()
+    # one row without a limit (k = V): the wide path, launched directly
+    SW = klein_amd.Sampler(W.Params(temperature=1.0, top_k=0, top_p=0.95), n_vocab=V, max_rows=1)
+    assert SW.path == "wide"
+    o1 = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    f1 = torch.full((1,), -2, dtype=torch.int32, device="cuda")
+    cs = torch.cuda.current_stream()
+    sc = C.c_void_p(cs.cuda_stream)  # (the events below are recorded on this stream)
+    _lib.check(L.kls_sample_batch(SW._h, dptr, 1, V, None, None, pb(ub), pb(f1), sc), "kls_sample_batch")
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cs)
+    for _ in range(10):
+        _lib.check(L.kls_sample_batch(SW._h, dptr, 1, V, None, None, pb(ub), pb(o1), sc), "kls_sample_batch")
+    e1.record(cs)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, f1), "wide row"
+    res["one_row_no_limit"] = {"path": "wide", "us": round(e0.elapsed_time(e1) * 1e3 / 10, 1)}
+    SW.close()
+    return res
+
+
 def host_info():
     info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "machine": platform.machine()}
     try:
@@ -502,6 +576,8 @@ def main():
     # ---------------- the next rows of the path: draft argmax, ppl scoring, rollback
     if not a.no_next:
         out["next_rows"] = next_rows(torch, klein_amd, W)
+    if not a.no_extra:
+        out["topk_above_64"] = topk_above_64(torch, klein_amd, W)
 
     out["copy_probe"] = copy_probe(torch, stream)
     if not a.no_cpu:

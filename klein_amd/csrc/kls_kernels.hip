@@ -1520,14 +1520,39 @@ __device__ __forceinline__ ParMap par_compose(const ParMap& e, const ParMap& l) 
     return c;
 }
 
-__device__ __forceinline__ long long shfl_up_ll(long long v, int d) {
-    const int lo = __shfl_up((int) (unsigned long long) v, (unsigned) d, 64);
-    const int hi = __shfl_up((int) ((unsigned long long) v >> 32), (unsigned) d, 64);
-    return (long long) (((unsigned long long) (unsigned) hi << 32) | (unsigned) lo);
+// A map moved across lanes by DPP control CTRL (rows ROWS enabled); lanes with no source (or a disabled row)
+// get the identity map.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ long long dpp_ll0(long long v) {
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) (unsigned long long) v, CTRL, ROWS, 0xf, false);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) ((unsigned long long) v >> 32), CTRL, ROWS, 0xf, false);
+    return (long long) (((unsigned long long) hi << 32) | lo);
 }
 
-__device__ __forceinline__ ParMap shfl_up_map(const ParMap& m, int d) {
-    return ParMap{shfl_up_ll(m.d0, d), shfl_up_ll(m.d1, d), (uint32_t) __shfl_up((int) m.p, (unsigned) d, 64)};
+template <int CTRL, int ROWS>
+__device__ __forceinline__ ParMap dpp_map(const ParMap& m) {
+    return ParMap{dpp_ll0<CTRL, ROWS>(m.d0), dpp_ll0<CTRL, ROWS>(m.d1),
+                  (uint32_t) __builtin_amdgcn_update_dpp(2, (int) m.p, CTRL, ROWS, 0xf, false)};
+}
+
+// Inclusive scan of the maps across lanes in lane order (earlier lanes' terms first): row_shr 1, 2, 4, 8 within
+// rows of 16, then row_bcast 15 and 31 (as wave_scan_f64). ROWS16: lanes 0..15 only (a scan of one row).
+template <bool ROWS16>
+__device__ __forceinline__ ParMap wave_scan_map(ParMap x) {
+    x = par_compose(dpp_map<0x111, 0xf>(x), x);
+    x = par_compose(dpp_map<0x112, 0xf>(x), x);
+    x = par_compose(dpp_map<0x114, 0xf>(x), x);
+    x = par_compose(dpp_map<0x118, 0xf>(x), x);
+    if (!ROWS16) {
+        x = par_compose(dpp_map<0x142, 0xa>(x), x);
+        x = par_compose(dpp_map<0x143, 0xc>(x), x);
+    }
+    return x;
+}
+
+__device__ __forceinline__ ParMap rdlane_map(const ParMap& m, int l) {
+    return ParMap{(long long) rdlane64((uint64_t) m.d0, l), (long long) rdlane64((uint64_t) m.d1, l),
+                  (uint32_t) __builtin_amdgcn_readlane((int) m.p, l)};
 }
 
 __shared__ ParMap s_rp_wave[TAIL_WG / 64];
@@ -1585,20 +1610,19 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
                 }
             }
         }
-        // workgroup inclusive scan of the maps (waves, then the waves' totals)
-        ParMap x = m;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const ParMap y = shfl_up_map(x, d);
-            if (lane >= d) x = par_compose(y, x);
+        // workgroup scan of the maps: each wave's (DPP; a wave past the terms holds identities and skips it),
+        // then the waves' totals (a 16-lane DPP scan that every wave runs on the totals it reads back)
+        ParMap x = par_identity(), xe = par_identity();
+        if (i + wave * 64 < n) {  // (uniform in the wave)
+            x = wave_scan_map<false>(m);
+            xe = dpp_map<0x138, 0xf>(x);  // wave_shr:1: the maps before this lane (lane 0: identity)
         }
-        ParMap xe = shfl_up_map(x, 1);
-        if (lane == 0) xe = par_identity();
         if (lane == 63) s_rp_wave[wave] = x;
         if (tid == 0) s_rp_first = 0x7fffffff;
         __syncthreads();
-        ParMap pre = par_identity();
-        for (int w2 = 0; w2 < wave; ++w2) pre = par_compose(pre, s_rp_wave[w2]);
+        const ParMap wt = wave_scan_map<true>(lane < TAIL_WG / 64 ? s_rp_wave[lane & (TAIL_WG / 64 - 1)] : par_identity());
+        const ParMap pre = wave == 0 ? par_identity() : rdlane_map(wt, wave - 1);
+        const ParMap tot_all = rdlane_map(wt, TAIL_WG / 64 - 1);
         const ParMap X = par_compose(pre, xe);  // the terms before j in this block
         const long long Aj = A0 + (pi0 ? X.d1 : X.d0);
         const uint32_t pij = pi0 ? ((X.p >> 1) & 1u) : (X.p & 1u);
@@ -1611,9 +1635,7 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
         const int first = s_rp_first;
         if (first == 0x7fffffff) {
             // no term left the binade or stopped: the block's total
-            ParMap tot = par_identity();
-            for (int w2 = 0; w2 < TAIL_WG / 64; ++w2) tot = par_compose(tot, s_rp_wave[w2]);
-            acc = (double) (A0 + (pi0 ? tot.d1 : tot.d0)) * u;
+            acc = (double) (A0 + (pi0 ? tot_all.d1 : tot_all.d0)) * u;
             i += TAIL_WG;
         } else {
             if (tid == first) {
@@ -1656,6 +1678,114 @@ __global__ __launch_bounds__(TAIL_WG) void sum_replay_kernel(const double* t, in
     }
 }
 
+// ---- Exact parallel forms of the tail's sums (one candidate per thread). The reference's chains add floats (e_i,
+// then p_i) in double. Every float term is a multiple of 2^g, g = the exponent of the least positive term - 23
+// (2^-149 for a subnormal least term); while a partial sum stays below 2^(g + 53) it is a multiple of 2^g with at
+// most 53 significant bits, so it is exact. Hence, when the whole sum is below 2^(g + 53), every partial sum in
+// any order is exact: the total is a tree reduction and the cumulative sums are a prefix scan. The test uses the
+// tree total with a factor-two margin (its rounding error, when there is any, is far below that).
+__shared__ double s_tx_sum[TAIL_WG / 64], s_tx_min[TAIL_WG / 64], s_tx_tot[TAIL_WG / 64], s_tx_pmin[TAIL_WG / 64];
+__shared__ int s_tx_mp[TAIL_WG / 64], s_tx_tp[TAIL_WG / 64], s_tx_dr[TAIL_WG / 64];
+
+// Least positive x across the wave (+inf when none).
+__device__ __forceinline__ double wave_min_pos(double x, int lane) {
+    uint64_t b = __builtin_bit_cast(uint64_t, x > 0.0 ? x : (double) INFINITY);
+    b = min64(b, xor_lane64<32>(b, lane));  // (positive doubles order as their bit patterns)
+    b = min64(b, xor_lane64<16>(b, lane));
+    b = min64(b, xor_lane64<8>(b, lane));
+    b = min64(b, xor_lane64<4>(b, lane));
+    b = min64(b, xor_lane64<2>(b, lane));
+    b = min64(b, xor_lane64<1>(b, lane));
+    return __builtin_bit_cast(double, b);
+}
+
+// The condition above for float terms whose least positive value is mn and whose tree total is tot.
+__device__ __forceinline__ bool sums_exact(double mn, double tot) {
+    if (!(mn < (double) INFINITY)) return true;  // no positive term: every partial sum is 0
+    int e;
+    (void) frexp(mn, &e);                        // mn in [2^(e-1), 2^e)
+    const int g = max(e - 1 - 23, -149);
+    return tot < ldexp(1.0, g + 52);
+}
+
+// The tail's sums with one candidate per thread (kk <= TAIL_WG, t[i] = e_i), four barriers: the softmax total
+// and its least term; p_i, the min-p cut, the cumulative sums, their total and least term; the top-p stop
+// (t[i] <- cum_i); the draw. Returns the drawn candidate with *n_kept and this thread's p_i, or -1 (t untouched)
+// when a chain is not exact in every order and must be replayed. The exactness of the cumulative chain is
+// judged over all kk terms, which covers the kept prefix.
+__device__ int tail_exact(double* t, int kk, const SamplingParams& p, double u, int lane, int wave, int* n_kept,
+                          float* p_mine) {
+    const int tid = (int) threadIdx.x;
+    const bool in = tid < kk;
+    const double e = in ? t[tid] : 0.0;
+    const double e0 = t[0];
+    {
+        const double sw = wave_sum_f64(e, lane), mw = wave_min_pos(e, lane);
+        if (lane == 0) {
+            s_tx_sum[wave] = sw;
+            s_tx_min[wave] = mw;
+        }
+    }
+    __syncthreads();
+    double sum = 0.0, mn = (double) INFINITY;
+#pragma unroll
+    for (int w = 0; w < TAIL_WG / 64; ++w) {
+        sum += s_tx_sum[w];
+        mn = fmin(mn, s_tx_min[w]);
+    }
+    if (!sums_exact(mn, sum)) return -1;
+    // p_i (:60) and min-p (:62-68): the first i >= 1 with p_i < p_0 * min_p ends the list
+    const float pf = in ? __double2float_rn(__ddiv_rn(e, sum)) : 0.0f;
+    const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
+    const uint64_t bm = ballot(p.min_p > 0.0f && in && tid >= 1 && !(pf >= thr));
+    const double x = in ? (double) pf : 0.0;
+    const double cw = wave_scan_f64(x);
+    {
+        const double tw = rdlaned(cw, 63), mw = wave_min_pos(x, lane);
+        if (lane == 0) {
+            s_tx_tot[wave] = tw;
+            s_tx_pmin[wave] = mw;
+            s_tx_mp[wave] = bm ? wave * 64 + __builtin_ctzll(bm) : 0x7fffffff;
+        }
+    }
+    __syncthreads();
+    double before = 0.0, tot = 0.0, pmn = (double) INFINITY;
+    int n = kk;
+#pragma unroll
+    for (int w = 0; w < TAIL_WG / 64; ++w) {
+        const double v = s_tx_tot[w];
+        before += w < wave ? v : 0.0;
+        tot += v;
+        pmn = fmin(pmn, s_tx_pmin[w]);
+        n = min(n, s_tx_mp[w]);
+    }
+    if (!sums_exact(pmn, tot)) return -1;
+    // top-p (:69-79): the first i with cum_i >= top_p keeps i + 1; the draw total (:80-81) is cum_{n-1}
+    const double cum = before + cw;
+    if (in) t[tid] = cum;  // (every thread read e_0 before the barrier above)
+    const uint64_t bt = ballot(tid < n && cum >= (double) p.top_p);
+    if (lane == 0) s_tx_tp[wave] = bt ? wave * 64 + __builtin_ctzll(bt) : 0x7fffffff;
+    __syncthreads();
+    if (p.top_p < 1.0f) {
+        int f = 0x7fffffff;
+#pragma unroll
+        for (int w = 0; w < TAIL_WG / 64; ++w) f = min(f, s_tx_tp[w]);
+        if (f != 0x7fffffff) n = f + 1;
+    }
+    // draw (:82-88): r = u*(total-0)+0; r - cum_i is exact while positive and keeps its sign at the step where it
+    // reaches <= 0, so the drawn candidate is the first i with cum_i >= r (the last kept if none)
+    const double r0 = __dadd_rn(__dmul_rn(u, __dsub_rn(t[n - 1], 0.0)), 0.0);
+    const uint64_t bd = ballot(tid < n && cum >= r0);
+    if (lane == 0) s_tx_dr[wave] = bd ? wave * 64 + __builtin_ctzll(bd) : 0x7fffffff;
+    __syncthreads();
+    int f = 0x7fffffff;
+#pragma unroll
+    for (int w = 0; w < TAIL_WG / 64; ++w) f = min(f, s_tx_dr[w]);
+    *n_kept = n;
+    *p_mine = pf;
+    return f != 0x7fffffff ? f : n - 1;
+}
+
 // Key layouts the tail reads: the wide path's packed keys, and the fast path's (value image << 32 | ~id).
 struct WideKeyFmt {
     int ib;          // id bits
@@ -1672,7 +1802,8 @@ struct FastKeyFmt {
 // The tail of src/sampler.cpp:53-88 over a row's sorted keys K (value descending, id ascending; the first k are
 // the candidates, ended early by the first key of value image 0, a NaN), with the whole workgroup (TAIL_WG
 // threads, uniform control flow): the per-candidate terms (e_i, then p_i) go to t[0..k) as doubles, and every sum
-// is the reference's sequential double chain replayed exactly (replay_sum). Publishes the row's token.
+// is the reference's sequential double chain: tail_exact when at most TAIL_WG candidates meet the exactness
+// condition above, else replayed exactly (replay_sum). Publishes the row's token.
 template <typename Fmt>
 __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k, double* t, const CallIn& cin,
                             const Fmt& fmt) {
@@ -1705,41 +1836,46 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
     }
     __syncthreads();
     const int kk = s_wide_n;
-    // the softmax total (:58), in reference order (exact replay)
-    int st;
-    const double sum = replay_sum(t, kk, 0.0, [](double, int) { return false; }, &st);
-    // p_i (:60), and min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
-    const double e0 = (double) expf_glibc(__fdiv_rn(__fsub_rn(maxl, maxl), p.temperature));
-    const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
-    if (tid == 0) s_wide_n = kk;
-    __syncthreads();
-    for (int i = tid; i < kk; i += TAIL_WG) {
-        const float pi = __double2float_rn(__ddiv_rn(t[i], sum));
-        if (p.min_p > 0.0f && i >= 1 && !(pi >= thr)) atomicMin(&s_wide_n, i);
-        t[i] = (double) pi;
-    }
-    __syncthreads();
-    int n = s_wide_n;
-    // top-p (:69-79): cum over the candidates until it reaches top_p; the draw total (:80-81) is the same chain
-    // over the kept ones
-    double total;
-    if (p.top_p < 1.0f) {
-        const double tp = (double) p.top_p;
-        total = replay_sum(t, n, 0.0, [tp](double acc, int) { return acc >= tp; }, &st);
-        n = st >= 0 ? st + 1 : n;
-    } else {
-        total = replay_sum(t, n, 0.0, [](double, int) { return false; }, &st);
-    }
-    // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a chain
-    // of additions of -p_i (exactly the subtractions)
-    const double r0 = __dadd_rn(__dmul_rn(cin.u, __dsub_rn(total, 0.0)), 0.0);
+    int n = 0;
+    float dbg_p = 0.0f;
+    int idx = kk <= TAIL_WG ? tail_exact(t, kk, p, cin.u, lane, wave, &n, &dbg_p) : -1;
     const bool act = lane < kk;
-    const float dbg_p = act ? (float) t[lane] : 0.0f;
-    __syncthreads();  // (every thread has read its p_i for the debug copy)
-    for (int i = tid; i < n; i += TAIL_WG) t[i] = -t[i];  // (p_i negated in place for the chain)
-    __syncthreads();
-    replay_sum(t, n, r0, [](double r, int) { return r <= 0.0; }, &st);
-    const int idx = st >= 0 ? st : n - 1;
+    if (idx < 0) {
+        // the chains replayed exactly in reference order: the softmax total (:58)
+        int st;
+        const double sum = replay_sum(t, kk, 0.0, [](double, int) { return false; }, &st);
+        // p_i (:60), and min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
+        const double e0 = (double) expf_glibc(__fdiv_rn(__fsub_rn(maxl, maxl), p.temperature));
+        const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
+        if (tid == 0) s_wide_n = kk;
+        __syncthreads();
+        for (int i = tid; i < kk; i += TAIL_WG) {
+            const float pi = __double2float_rn(__ddiv_rn(t[i], sum));
+            if (p.min_p > 0.0f && i >= 1 && !(pi >= thr)) atomicMin(&s_wide_n, i);
+            t[i] = (double) pi;
+        }
+        __syncthreads();
+        n = s_wide_n;
+        dbg_p = act ? (float) t[lane] : 0.0f;
+        // top-p (:69-79): cum over the candidates until it reaches top_p; the draw total (:80-81) is the same
+        // chain over the kept ones
+        double total;
+        if (p.top_p < 1.0f) {
+            const double tp = (double) p.top_p;
+            total = replay_sum(t, n, 0.0, [tp](double acc, int) { return acc >= tp; }, &st);
+            n = st >= 0 ? st + 1 : n;
+        } else {
+            total = replay_sum(t, n, 0.0, [](double, int) { return false; }, &st);
+        }
+        // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a
+        // chain of additions of -p_i (exactly the subtractions)
+        const double r0 = __dadd_rn(__dmul_rn(cin.u, __dsub_rn(total, 0.0)), 0.0);
+        __syncthreads();  // (every thread has read its p_i for the debug copy)
+        for (int i = tid; i < n; i += TAIL_WG) t[i] = -t[i];  // (p_i negated in place for the chain)
+        __syncthreads();
+        replay_sum(t, n, r0, [](double r, int) { return r <= 0.0; }, &st);
+        idx = st >= 0 ? st : n - 1;
+    }
     if (wave != 0) return;
     const int tok = fmt.id(K[idx]);
     const uint64_t kl = act ? K[lane] : 0ull;
@@ -1777,8 +1913,8 @@ __global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs
 //   4. the keys that reach it are appended to the row's buffer (space taken with a device-scope counter), so the
 //      buffer holds every key of the row's top k;
 //   5. the row's last workgroup (ticket) holds the buffer in registers (16 keys per thread), forms the same
-//      bound for k over it (bisected down to MID_SORT keys if needed), sorts the keys that reach it in LDS and
-//      runs sorted_tail over the first k.
+//      bound for k over it when it holds more than 2k + 256 keys (bisected down to MID_SORT keys if needed),
+//      sorts the keys that reach it in LDS and runs sorted_tail over the first k.
 // Counters are left zero for the next launch (the ticket by publish, the buffer's counter by the last workgroup).
 constexpr int MID_NW = 16, MID_WG = MID_NW * 64, MID_EPT = 32, MID_RK = MID_ROWCAP / MID_WG;
 constexpr int MID_SORT = 4096;  // keys the row's sort holds
@@ -2054,7 +2190,7 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
         return c;
     };
     uint64_t T2 = 1ull;  // (every buffered key: all are numbers)
-    if (N > MID_SORT) {
+    if (N > 2 * k + 256) {  // (always when N > MID_SORT)
         uint32_t q1 = 0u, q2 = 0u;
 #pragma unroll
         for (int r = 0; r < MID_RK; ++r) {
