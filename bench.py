@@ -148,6 +148,7 @@ def next_rows(torch, klein_amd, W):
     g = W.greedy()
     d1 = torch.from_numpy(g.logits).cuda()
     o1 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()  # (buffers made on torch's stream, used on others: ready before any launch)
     us = graph_us(torch, lambda sp: _lib.check(L.kls_argmax(h, p(d1), 1, V, p(o1), sp), "kls_argmax"), 200)
     assert int(o1.item()) == g.expected_greedy
     res["draft_argmax"] = {"workload": "1 row x 248,320 f32 (std::max_element)", "us": round(us, 2),
@@ -161,6 +162,7 @@ def next_rows(torch, klein_amd, W):
     tg = torch.from_numpy(rng.integers(0, V, 64).astype(np.int32)).cuda()
     outs = [torch.empty(64, dtype=torch.float64, device="cuda") for _ in range(4)]
     tops = [torch.empty(64, dtype=torch.int32, device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
     k = [0]
 
     def ppl(sp):
@@ -188,6 +190,7 @@ def next_rows(torch, klein_amd, W):
     rh = C.c_void_p()
     _lib.check(L.kls_recurrent_create(C.byref(desc), C.byref(rh)), "kls_recurrent_create")
     acc = torch.tensor([1], dtype=torch.int32, device="cuda")  # accepted 1 of 3 drafts: s = 2
+    torch.cuda.synchronize()
     us = graph_us(torch, lambda sp: _lib.check(L.kls_rollback_recurrent(rh, p(acc), 4, sp), "kls_rollback"), 20)
     L.kls_recurrent_destroy(rh)
     res["rollback"] = {"workload": "48 DeltaNet layers (conv 30,720 f32 slot copy, ssm 786,432 f16 -> f32), s = 2",
@@ -242,6 +245,7 @@ def topk_above_64(torch, klein_amd, W):
     ub = torch.from_numpy(wb.u).cuda()
     ob = torch.full((64,), -1, dtype=torch.int32, device="cuda")
     first = torch.full((64,), -2, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()  # (made on torch's stream, written on the library's and on another)
     pb = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
     _lib.check(L.kls_sample_batch(SB._h, pb(xb), 64, V, None, None, pb(ub), pb(first), None), "kls_sample_batch")
     us_b = graph_us(torch, lambda s: _lib.check(L.kls_sample_batch(SB._h, pb(xb), 64, V, None, None, pb(ub), pb(ob),
@@ -538,6 +542,7 @@ def main():
         outp = [C.c_void_p(outs[i].data_ptr()) for i in range(n_b + 20)]
         # expected tokens per input set, from untimed launches
         expd = torch.full((n_sets, 64), -2, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()  # (inputs and outputs made on torch's stream, used on the bench stream)
         for j in range(n_sets):
             _lib.check(L.kls_sample_batch(hb, ptrs[j], 64, V, offp, idsp, up, C.c_void_p(expd[j].data_ptr()), sp),
                        "kls_sample_batch")

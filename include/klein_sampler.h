@@ -46,7 +46,8 @@ typedef struct kls_params {
 typedef struct kls_sampler* kls_handle;
 
 /* hipStream_t, passed as a plain pointer; NULL selects the library's own stream of the handle's device (one per
- * device, shared by every handle created on it). */
+ * device, shared by every handle created on it; a blocking stream, so such calls are ordered with work on the
+ * legacy default stream). */
 typedef void* kls_stream;
 
 /* Replaces Sampler::Sampler (src/sampler.cpp:11). Binds the current HIP device, allocates every buffer the

@@ -190,12 +190,13 @@ std::unordered_set<hipStream_t> g_graph_ready;   // streams that have carried PR
 
 // The library's own stream of `device` (created on first use, kept for the process): handles created without
 // a caller stream share it, so a new handle costs no stream creation and starts on a stream that is ready for
-// graph launches.
+// graph launches. A blocking stream: like work passed the NULL stream, it is ordered with the legacy default
+// stream (a caller's buffers filled there are ready before a call reads or writes them).
 hipError_t library_stream(int device, hipStream_t* out) {
     if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_mu);
     if (!g_stream[device]) {
-        const hipError_t e = hipStreamCreateWithFlags(&g_stream[device], hipStreamNonBlocking);
+        const hipError_t e = hipStreamCreateWithFlags(&g_stream[device], hipStreamDefault);
         if (e != hipSuccess) {
             g_stream[device] = nullptr;
             return e;

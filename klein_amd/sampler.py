@@ -33,6 +33,20 @@ def _stream_ptr(stream):
     return C.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
 
 
+def _call_stream(stream, like):
+    """The stream a device call runs on: `stream` if given; else, for torch tensor arguments, torch's current
+    stream, so that the call is ordered with the torch work that makes and reads its buffers (as a torch op
+    is); else NULL. (torch's default stream is the legacy default stream, handle 0: NULL then selects the
+    library's stream, which is ordered with it.)"""
+    if stream is not None:
+        return _stream_ptr(stream)
+    if hasattr(like, "data_ptr") and getattr(like, "is_cuda", False):
+        import torch
+        cs = torch.cuda.current_stream(like.device).cuda_stream
+        return C.c_void_p(cs) if cs else None
+    return None
+
+
 class Sampler:
     """klein::Sampler. max_rows bounds verify()/sample_batch() rows."""
 
@@ -155,7 +169,7 @@ class Sampler:
         _lib.check(_lib.lib().kls_verify(self._h, _ptr(logits), nb, dr.ctypes.data_as(C.POINTER(C.c_int32)),
                                          uu.ctypes.data_as(C.POINTER(C.c_double)),
                                          toks.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(acc),
-                                         _stream_ptr(stream)), "kls_verify")
+                                         _call_stream(stream, logits)), "kls_verify")
         a = int(acc.value)
         if consume and self._p.temperature > 0:
             self._rng.discard(a + 1)
@@ -163,14 +177,15 @@ class Sampler:
 
     def sample_batch(self, logits, u, out_tokens, hist_off=None, hist_ids=None, stream=None):
         """Independent rows on the device (torch tensors): logits [rows, V] f32, u [rows] f64, out [rows] i32,
-        optional CSR histories hist_off [rows+1] i32 / hist_ids i32. Asynchronous on `stream`."""
+        optional CSR histories hist_off [rows+1] i32 / hist_ids i32. Asynchronous on `stream` (default: torch's
+        current stream)."""
         rows, n = int(logits.shape[0]), int(logits.shape[1])
         self._ensure(n)
         stride = int(logits.stride(0)) if hasattr(logits, "stride") else n
         _lib.check(_lib.lib().kls_sample_batch(
             self._h, _ptr(logits), rows, stride, None if hist_off is None else _ptr(hist_off),
             None if hist_ids is None else _ptr(hist_ids), None if u is None else _ptr(u), _ptr(out_tokens),
-            _stream_ptr(stream)), "kls_sample_batch")
+            _call_stream(stream, out_tokens)), "kls_sample_batch")
 
     def argmax(self, logits, out, stream=None):
         """Engine::mtp_draft_token (src/engine.cpp:413-415) per row of the device tensor logits [rows, V] f32:
@@ -178,7 +193,7 @@ class Sampler:
         rows, n = int(logits.shape[0]), int(logits.shape[1])
         self._ensure(n)
         stride = int(logits.stride(0)) if hasattr(logits, "stride") else n
-        _lib.check(_lib.lib().kls_argmax(self._h, _ptr(logits), rows, stride, _ptr(out), _stream_ptr(stream)),
+        _lib.check(_lib.lib().kls_argmax(self._h, _ptr(logits), rows, stride, _ptr(out), _call_stream(stream, out)),
                    "kls_argmax")
 
     def ppl_scores(self, logits, targets, base=None, stream=None):
@@ -200,7 +215,7 @@ class Sampler:
         _lib.check(_lib.lib().kls_ppl_scores(
             self._h, _ptr(logits), rows, int(logits.stride(0)), _ptr(targets),
             None if base is None else _ptr(base), int(base.stride(0)) if base is not None else 0,
-            g("lse"), g("nll"), g("top"), g("kl"), g("nll_base"), g("base_top"), _stream_ptr(stream)),
+            g("lse"), g("nll"), g("top"), g("kl"), g("nll_base"), g("base_top"), _call_stream(stream, logits)),
             "kls_ppl_scores")
         return out
 
@@ -222,12 +237,12 @@ def debug_sum_replay(terms, acc0: float, mode: int = 0, thr: float = 0.0, stream
     import torch
     out = torch.zeros(2, dtype=torch.float64, device=terms.device)
     _lib.check(_lib.lib().kls_debug_sum_replay(_ptr(terms), int(terms.numel()), float(acc0), int(mode), float(thr),
-                                               _ptr(out), _stream_ptr(stream)), "kls_debug_sum_replay")
+                                               _ptr(out), _call_stream(stream, out)), "kls_debug_sum_replay")
     r = out.cpu().numpy()
     return float(r[0]), int(r[1])
 
 
 def debug_expf(lo_bits: int, out, stream=None):
     """Device expf of float bit patterns lo_bits .. lo_bits+len(out)-1 into the torch float32 tensor `out`."""
-    _lib.check(_lib.lib().kls_debug_expf(int(lo_bits), int(out.numel()), _ptr(out), _stream_ptr(stream)),
+    _lib.check(_lib.lib().kls_debug_expf(int(lo_bits), int(out.numel()), _ptr(out), _call_stream(stream, out)),
                "kls_debug_expf")
