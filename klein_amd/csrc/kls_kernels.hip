@@ -1499,10 +1499,10 @@ __shared__ int s_wide_n;  // kk, then the min-p length
 // integer in [2^52, 2^53), and RN(A*u + t) = (A + d)*u where, writing t/u = f + phi (f integer, 0 <= phi < 1),
 // d = f when phi < 1/2, f + 1 when phi > 1/2, and at a tie (phi = 1/2) whichever of f, f + 1 makes A + d even.
 // So each term is a map of the parity of A: (d for parity 0, d for parity 1, parity after each). Maps compose
-// associatively, so a workgroup scans 1,024 terms at a time and knows every A on the way. A term whose exact
-// sum could leave the binade (A + f < 2^52, or A + f >= 2^53 - 1, or t/u huge) is added with the real double
-// addition instead, and the scan restarts after it in the new binade; so is every term while acc is 0 or
-// subnormal. Identical results to the sequential loop, in ~250 workgroup steps for 248,320 terms.
+// associatively, so a workgroup scans 8,192 terms at a time (8 per thread) and knows every A on the way. A term
+// whose exact sum could leave the binade (A + f < 2^52, or A + f >= 2^53 - 1, or t/u huge) is added with the real
+// double addition instead, and the scan restarts after it in the new binade; so is every term while acc is 0 or
+// subnormal. Identical results to the sequential loop, in ~31 workgroup steps for 248,320 terms.
 struct ParMap {
     long long d0, d1;  // increments (in units of u) for incoming parity 0 / 1
     uint32_t p;        // bit 0: parity after, from parity 0; bit 1: from parity 1
@@ -1560,6 +1560,38 @@ __shared__ int s_rp_first;
 __shared__ double s_rp_acc;
 __shared__ int s_rp_next, s_rp_stop;
 
+// The map of one term t in the binade of 2^E (f: its integer part in units of u; cross: too large to map).
+__device__ __forceinline__ ParMap term_map(double t, int E, long long* f, bool* cross) {
+    const double q = ldexp(t, 52 - E);
+    ParMap m = par_identity();
+    *f = 0;
+    *cross = false;
+    if (!(fabs(q) < 0x1p62)) {
+        *cross = true;  // (handled by the real addition; the map is not used past it)
+        return m;
+    }
+    const double fl = floor(q);
+    const long long fi = (long long) fl;
+    *f = fi;
+    const double ph = q - fl;  // exact
+    if (ph == 0.5) {
+        m.d0 = fi + (fi & 1);
+        m.d1 = fi + ((fi + 1) & 1);
+        m.p = 0u;
+    } else {
+        const long long d = fi + (ph > 0.5 ? 1 : 0);
+        m.d0 = m.d1 = d;
+        m.p = (uint32_t) (d & 1) | ((uint32_t) ((d + 1) & 1) << 1);
+    }
+    return m;
+}
+
+// Terms per thread in one block of the replay: thread tid takes RP_PT consecutive terms, composes their maps in
+// registers, and the workgroup scans the threads' maps, so a block covers TAIL_WG * RP_PT terms with one scan and
+// two barriers; each thread then walks its own terms from the scanned prefix to find the first that leaves the
+// binade or meets the stop (the terms are read again rather than held).
+constexpr int RP_PT = 8;
+
 // Replays the chain over t[0..n) from `acc` with the whole workgroup (every thread calls it, uniformly);
 // stop(acc, i) is evaluated on each partial result after term i, and the first i for which it holds ends the
 // chain (returned in *stopped, else -1). Returns the last partial result.
@@ -1585,36 +1617,22 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
         const double u = ldexp(1.0, E - 52);
         const long long A0 = (long long) ldexp(acc, 52 - E);
         const uint32_t pi0 = (uint32_t) (A0 & 1);
-        const int j = i + tid;
-        const bool in = j < n;
-        const double tj = in ? t[j] : 0.0;
-        const double q = ldexp(tj, 52 - E);
-        bool cross = false;
-        long long f = 0;
-        ParMap m = par_identity();
-        if (in) {
-            if (!(fabs(q) < 0x1p62)) {
-                cross = true;  // (handled by the real addition; the map is not used past it)
-            } else {
-                const double fl = floor(q);
-                f = (long long) fl;
-                const double ph = q - fl;  // exact
-                if (ph == 0.5) {
-                    m.d0 = f + (f & 1);
-                    m.d1 = f + ((f + 1) & 1);
-                    m.p = 0u;
-                } else {
-                    const long long d = f + (ph > 0.5 ? 1 : 0);
-                    m.d0 = m.d1 = d;
-                    m.p = (uint32_t) (d & 1) | ((uint32_t) ((d + 1) & 1) << 1);
-                }
+        const int j0 = i + tid * RP_PT;
+        // the composed map of this thread's terms
+        ParMap M = par_identity();
+#pragma unroll
+        for (int q = 0; q < RP_PT; ++q) {
+            if (j0 + q < n) {
+                long long f;
+                bool c;
+                M = par_compose(M, term_map(t[j0 + q], E, &f, &c));
             }
         }
-        // workgroup scan of the maps: each wave's (DPP; a wave past the terms holds identities and skips it),
-        // then the waves' totals (a 16-lane DPP scan that every wave runs on the totals it reads back)
+        // workgroup scan of the threads' maps: each wave's (DPP; a wave past the terms holds identities and
+        // skips it), then the waves' totals (a 16-lane DPP scan that every wave runs on the totals it reads back)
         ParMap x = par_identity(), xe = par_identity();
-        if (i + wave * 64 < n) {  // (uniform in the wave)
-            x = wave_scan_map<false>(m);
+        if (i + wave * 64 * RP_PT < n) {  // (uniform in the wave)
+            x = wave_scan_map<false>(M);
             xe = dpp_map<0x138, 0xf>(x);  // wave_shr:1: the maps before this lane (lane 0: identity)
         }
         if (lane == 63) s_rp_wave[wave] = x;
@@ -1623,33 +1641,55 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
         const ParMap wt = wave_scan_map<true>(lane < TAIL_WG / 64 ? s_rp_wave[lane & (TAIL_WG / 64 - 1)] : par_identity());
         const ParMap pre = wave == 0 ? par_identity() : rdlane_map(wt, wave - 1);
         const ParMap tot_all = rdlane_map(wt, TAIL_WG / 64 - 1);
-        const ParMap X = par_compose(pre, xe);  // the terms before j in this block
-        const long long Aj = A0 + (pi0 ? X.d1 : X.d0);
-        const uint32_t pij = pi0 ? ((X.p >> 1) & 1u) : (X.p & 1u);
-        const long long dj = pij ? m.d1 : m.d0;
-        if (in && !cross) cross = (Aj + f < TWO52) || (Aj + f >= TWO53 - 1);
-        const double nxt = (double) (Aj + dj) * u;  // (exact when no earlier term crossed)
-        const bool hit = in && (cross || stop(nxt, j));
-        if (hit) atomicMin(&s_rp_first, j - i);
+        // this thread's terms in order, from the maps of every term before them in this block
+        ParMap X = par_compose(pre, xe);
+        int hq = -1;
+        bool h_cross = false;
+        long long h_A = 0;
+        double h_t = 0.0, h_nxt = 0.0;
+        for (int q = 0; q < RP_PT && j0 + q < n; ++q) {
+            const int j = j0 + q;
+            const double tj = t[j];
+            long long f;
+            bool cross;
+            const ParMap m = term_map(tj, E, &f, &cross);
+            const long long Aj = A0 + (pi0 ? X.d1 : X.d0);
+            const uint32_t pij = pi0 ? ((X.p >> 1) & 1u) : (X.p & 1u);
+            const long long dj = pij ? m.d1 : m.d0;
+            if (!cross) cross = (Aj + f < TWO52) || (Aj + f >= TWO53 - 1);
+            const double nxt = (double) (Aj + dj) * u;  // (exact when no earlier term crossed)
+            if (cross || stop(nxt, j)) {
+                hq = q;
+                h_cross = cross;
+                h_A = Aj;
+                h_t = tj;
+                h_nxt = nxt;
+                break;
+            }
+            X = par_compose(X, m);
+        }
+        if (hq >= 0) atomicMin(&s_rp_first, j0 + hq - i);
         __syncthreads();
         const int first = s_rp_first;
         if (first == 0x7fffffff) {
             // no term left the binade or stopped: the block's total
             acc = (double) (A0 + (pi0 ? tot_all.d1 : tot_all.d0)) * u;
-            i += TAIL_WG;
+            i += TAIL_WG * RP_PT;
         } else {
-            if (tid == first) {
+            if (hq >= 0 && j0 + hq - i == first) {
+                // (the thread that holds the first such term)
+                const int j = j0 + hq;
                 double r;
-                int nx = j + 1, s2 = -1;
-                if (cross) {
-                    r = __dadd_rn((double) Aj * u, tj);
+                int s2 = -1;
+                if (h_cross) {
+                    r = __dadd_rn((double) h_A * u, h_t);
                     if (stop(r, j)) s2 = j;
                 } else {
-                    r = nxt;
+                    r = h_nxt;
                     s2 = j;
                 }
                 s_rp_acc = r;
-                s_rp_next = nx;
+                s_rp_next = j + 1;
                 s_rp_stop = s2;
             }
             __syncthreads();
