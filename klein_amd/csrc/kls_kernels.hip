@@ -1586,16 +1586,15 @@ __device__ __forceinline__ ParMap term_map(double t, int E, long long* f, bool* 
     return m;
 }
 
-// Terms per thread in one block of the replay: thread tid takes RP_PT consecutive terms, composes their maps in
-// registers, and the workgroup scans the threads' maps, so a block covers TAIL_WG * RP_PT terms with one scan and
-// two barriers; each thread then walks its own terms from the scanned prefix to find the first that leaves the
-// binade or meets the stop (the terms are read again rather than held).
-constexpr int RP_PT = 8;
-
 // Replays the chain over t[0..n) from `acc` with the whole workgroup (every thread calls it, uniformly);
 // stop(acc, i) is evaluated on each partial result after term i, and the first i for which it holds ends the
 // chain (returned in *stopped, else -1). Returns the last partial result.
-template <typename F>
+// RP_PT terms per thread in one block: thread tid takes RP_PT consecutive terms, composes their maps in
+// registers, and the workgroup scans the threads' maps, so a block covers TAIL_WG * RP_PT terms with one scan and
+// two barriers; each thread then walks its own terms from the scanned prefix to find the first that leaves the
+// binade or meets the stop (the terms are read again rather than held). 8 suits long chains (a pass is bound by
+// one CU's VALU time, the scans and barriers amortized), 1 chains of at most TAIL_WG terms (no serial walk).
+template <int RP_PT, typename F>
 __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F stop, int* stopped) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr long long TWO52 = 1ll << 52, TWO53 = 1ll << 53;
@@ -1704,14 +1703,15 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
     return acc;
 }
 
-// Test hook: replay_sum over t[0..n) from acc0; mode 0 never stops, 1 stops at acc >= thr, 2 at acc <= 0.
+// Test hook: replay_sum over t[0..n) from acc0 (8 terms per thread above TAIL_WG terms, else 1, as the tail
+// chooses); mode 0 never stops, 1 stops at acc >= thr, 2 at acc <= 0.
 // out[0] = the result, out[1] = the stop index (-1: none).
 __global__ __launch_bounds__(TAIL_WG) void sum_replay_kernel(const double* t, int n, double acc0, int mode, double thr,
                                                              double* out) {
     int st;
-    const double r = replay_sum(t, n, acc0, [mode, thr](double acc, int) {
-        return mode == 1 ? acc >= thr : mode == 2 ? acc <= 0.0 : false;
-    }, &st);
+    const auto stop = [mode, thr](double acc, int) { return mode == 1 ? acc >= thr : mode == 2 ? acc <= 0.0 : false; };
+    // (the tail's choice of terms per thread)
+    const double r = n > TAIL_WG ? replay_sum<8>(t, n, acc0, stop, &st) : replay_sum<1>(t, n, acc0, stop, &st);
     if (threadIdx.x == 0) {
         out[0] = r;
         out[1] = (double) st;
@@ -1883,7 +1883,8 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
     if (idx < 0) {
         // the chains replayed exactly in reference order: the softmax total (:58)
         int st;
-        const double sum = replay_sum(t, kk, 0.0, [](double, int) { return false; }, &st);
+        const auto never = [](double, int) { return false; };
+        const double sum = kk > TAIL_WG ? replay_sum<8>(t, kk, 0.0, never, &st) : replay_sum<1>(t, kk, 0.0, never, &st);
         // p_i (:60), and min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
         const double e0 = (double) expf_glibc(__fdiv_rn(__fsub_rn(maxl, maxl), p.temperature));
         const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
@@ -1902,10 +1903,11 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
         double total;
         if (p.top_p < 1.0f) {
             const double tp = (double) p.top_p;
-            total = replay_sum(t, n, 0.0, [tp](double acc, int) { return acc >= tp; }, &st);
+            const auto reach = [tp](double acc, int) { return acc >= tp; };
+            total = n > TAIL_WG ? replay_sum<8>(t, n, 0.0, reach, &st) : replay_sum<1>(t, n, 0.0, reach, &st);
             n = st >= 0 ? st + 1 : n;
         } else {
-            total = replay_sum(t, n, 0.0, [](double, int) { return false; }, &st);
+            total = n > TAIL_WG ? replay_sum<8>(t, n, 0.0, never, &st) : replay_sum<1>(t, n, 0.0, never, &st);
         }
         // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a
         // chain of additions of -p_i (exactly the subtractions)
@@ -1913,7 +1915,11 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
         __syncthreads();  // (every thread has read its p_i for the debug copy)
         for (int i = tid; i < n; i += TAIL_WG) t[i] = -t[i];  // (p_i negated in place for the chain)
         __syncthreads();
-        replay_sum(t, n, r0, [](double r, int) { return r <= 0.0; }, &st);
+        const auto spent = [](double r, int) { return r <= 0.0; };
+        if (n > TAIL_WG)
+            replay_sum<8>(t, n, r0, spent, &st);
+        else
+            replay_sum<1>(t, n, r0, spent, &st);
         idx = st >= 0 ? st : n - 1;
     }
     if (wave != 0) return;

@@ -2,7 +2,8 @@
 total, top-p cumulative sum and draw, src/sampler.cpp:58,70-77,84-87, accumulate one term at a time in double):
 the result and the stop index must equal a plain in-order loop of IEEE double additions (Python floats), bit for
 bit, on inputs built to hit every branch: round-to-even ties on every term, many binade crossings up and down,
-stops, huge and tiny terms, zero / subnormal / negative starting values, NaN and infinity."""
+stops, huge and tiny terms, zero / subnormal / negative starting values, NaN and infinity. Chains of more than
+1,024 terms run with 8 terms per thread, shorter ones with one (both forms are checked)."""
 import math
 
 import numpy as np
@@ -103,3 +104,25 @@ def test_specials(torch_cuda):
     check(torch_cuda, t, 0.0, 0, label="inf term")
     check(torch_cuda, np.full(4000, 2.0 ** -60), 1.0, 0, label="below half an ulp")
     check(torch_cuda, np.full(4000, 2.0 ** -53), 1.0, 0, label="exactly half an ulp")
+
+
+def test_short_chains(torch_cuda):
+    """The one-term-per-thread form (chains of at most 1,024 terms, as the mid top-k tail replays): pieces of the
+    patterns above, with ties, crossings, stops and a draw."""
+    rng = np.random.default_rng(6)
+    ties = (2 * rng.integers(0, 1 << 20, 1024) + 1).astype(np.float64) * 2.0 ** -53
+    up = rng.uniform(0, 10, 1000)
+    p = np.sort(rng.dirichlet(np.full(700, 0.3)))[::-1].astype(np.float32).astype(np.float64)
+    mixed = rng.standard_normal(1024) * 10.0 ** rng.uniform(-20, 5, 1024)
+    x = np.sort(rng.uniform(0, 40, 1024))
+    soft = np.exp(-x).astype(np.float32).astype(np.float64)
+    soft[0] = 1.0
+    say("short chains")
+    check(torch_cuda, ties, 1.0, 0, label="short ties")
+    check(torch_cuda, up, 0.0, 0, label="short up")
+    check(torch_cuda, up, 0.0, 1, 2500.5, label="short stop")
+    check(torch_cuda, p, 0.0, 1, 0.95, label="short top-p")
+    check(torch_cuda, -p, 0.37 * float(np.sum(p)), 2, label="short draw")
+    check(torch_cuda, mixed, 3.0, 0, label="short mixed")
+    check(torch_cuda, soft, 0.0, 0, label="short softmax")
+    check(torch_cuda, soft[:1], 0.0, 0, label="one term")
