@@ -73,6 +73,13 @@ int main(int argc, char** argv) {
         s.V = 5000; s.samples = 4; s.verifies = 2;
         sc.push_back(s);
     }
+    {
+        Scenario s{};  // top-k 300: the mid path
+        s.p.temperature = 0.8f; s.p.top_k = 300; s.p.top_p = 0.97f; s.p.min_p = 0.01f;
+        s.p.repetition_penalty = 1.05f; s.p.presence_penalty = 0.2f; s.p.seed = 9;
+        s.V = 248320; s.samples = 4; s.verifies = 3;
+        sc.push_back(s);
+    }
     std::mt19937_64 gen(20261201);
     for (size_t n = 0; n < sc.size(); ++n) {
         const Scenario& s = sc[n];

@@ -3,8 +3,8 @@ on the GPU against the reference's own Sampler (src/sampler.cpp compiled into or
 drives the drop-in through sample()/accept() and 4-row verify() steps with a fixed seed and records the logits,
 drafts and tokens; the reference replays each scenario with the same seed (the same mt19937_64 draws) through
 sample()/accept() and the engine's verify loop (src/engine.cpp:563-575). Tokens and accepted counts must match
-exactly. Scenarios: the verify configuration, penalties with min-p, greedy with a presence penalty, and no top-k
-limit (the wide path)."""
+exactly. Scenarios: the verify configuration, penalties with min-p, greedy with a presence penalty, no top-k
+limit (the wide path), and top-k 300 with min-p and penalties (the mid path)."""
 import os
 import subprocess
 import sys
@@ -70,4 +70,4 @@ def test_cpp_dropin_matches_reference(tmp_path):
                 assert st[2] == acc and st[3] == list(toks[:acc + 1]), (n, s, st, list(toks), acc)
         assert at == logits.size
         n += 1
-    assert n == 4
+    assert n == 5
