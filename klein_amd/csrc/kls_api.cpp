@@ -336,8 +336,11 @@ RowsArgs step_args(kls_sampler* h, const float* logits, int rows, bool verify) {
     return a;
 }
 
-// The sampling kernel of the handle's path over `a` (the fast path or the mid top-k path: one kernel each).
+// The sampling kernels of the handle's path over `a` (the fast path and the mid top-k path: one kernel each;
+// the wide path: keys, the radix sort's passes, the tail). None of them sets memory with a memset, so a verify
+// step of any path can be captured in a graph.
 hipError_t launch_sampling(const kls_sampler* h, const RowsArgs& a, bool penalize, hipStream_t s) {
+    if (h->wide) return launch_wide(a, h->w, penalize, s);
     if (h->mid) return launch_mid(a, h->m, penalize, s);
     return launch_rows(a, h->greedy, penalize, s);
 }
@@ -402,10 +405,7 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
     if (st) return st;
     h->call->seq = ++h->seq;
     const RowsArgs a = step_args(h, dl, rows, verify);
-    if (h->wide) {
-        // (several kernels and a library sort: launched directly, not captured)
-        KLS_HIP(launch_wide(a, h->w, h->penalize, s));
-    } else if (verify) {
+    if (verify) {
         if (!h->g_valid || h->g_logits != dl || h->g_rows != rows) {
             // (a stale graph is replaced whether or not its teardown reports an error)
             if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
@@ -517,7 +517,7 @@ int kls_destroy(kls_handle h) {
     void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_seg_cand,
                    h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_accepted,
                    h->d_step, h->d_dbg_keys, h->d_dbg_probs, h->d_dbg_meta,
-                   h->d_rows_buf, h->w.keys, h->w.sorted, h->w.sort_tmp, h->m.buf, h->m.fill};
+                   h->d_rows_buf, h->w.keys, h->w.sorted, h->w.counts, h->m.buf, h->m.fill};
     for (void* p : dev)
         if (p) (void) hipFree(p);
     if (h->h_stage) (void) hipHostFree(h->h_stage);
@@ -604,10 +604,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
         h->w.id_bits = wide_id_bits(n_vocab);
         ALLOC(h->w.keys, sizeof(uint64_t) * R * n_vocab);
         ALLOC(h->w.sorted, sizeof(uint64_t) * R * n_vocab);
-        if ((e = sort_keys_desc(nullptr, &h->w.sort_tmp_bytes, h->w.keys, h->w.sorted, R * n_vocab, 64, h->stream)) !=
-            hipSuccess)
-            return oom("sort scratch size", e);
-        ALLOC(h->w.sort_tmp, h->w.sort_tmp_bytes);
+        ALLOC(h->w.counts, sizeof(uint32_t) * 256 * sort_tiles(R * (size_t) n_vocab));
     }
 #undef ALLOC
     if ((e = hipHostMalloc((void**) &h->h_stage, sizeof(int32_t) * (2 * (size_t) n_vocab + h->n_buckets + 1),
@@ -758,10 +755,7 @@ int kls_sample_batch(kls_handle h, const float* d_logits, int n_rows, int64_t ro
     }
     a.u = d_u;
     a.out_tokens = d_out_tokens;
-    if (h->wide)
-        KLS_HIP(launch_wide(a, h->w, pen, s));
-    else
-        KLS_HIP(launch_sampling(h, a, pen, s));
+    KLS_HIP(launch_sampling(h, a, pen, s));
     return KLS_OK;
 }
 

@@ -127,10 +127,9 @@ constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 20;
 // value image 0, after every number. The sorted keys then go through the O(k) tail in reference order.
 struct WideArgs {
     uint64_t* keys;       // [n_rows * V]
-    uint64_t* sorted;     // [n_rows * V]
-    void* sort_tmp;       // device sort scratch
-    size_t sort_tmp_bytes;
-    int32_t k;            // KCAP < k <= V
+    uint64_t* sorted;     // [n_rows * V] (the sort alternates between the two buffers)
+    uint32_t* counts;     // the sort's digit counts: 256 * sort_tiles(max_rows * V)
+    int32_t k;            // MID_KMAX < k <= V (or a k the mid path cannot hold)
     int32_t id_bits;      // ids are below 1 << id_bits
 };
 
@@ -206,9 +205,12 @@ int wide_id_bits(int V);  // key bits the ids of a V-entry vocabulary take
 hipError_t launch_mid(const RowsArgs& a, const MidArgs& m, bool penalize, hipStream_t s);
 hipError_t prepare_mid_kernels();  // once per device: LDS limit of the kernel with a count table
 
-// Descending device-wide sort of n 64-bit keys on bits [0, end_bit) (kls_sort.hip). With tmp == nullptr, sets
-// *bytes to the scratch size.
-hipError_t sort_keys_desc(void* tmp, size_t* bytes, const uint64_t* in, uint64_t* out, size_t n, int end_bit,
+// Descending device-wide sort of n 64-bit keys (n < 2^32) on bits [0, end_bit) (kls_sort.hip): a stable radix
+// sort, 8 bits per pass, alternating between the buffers a (the input) and b; *result is the one that holds the
+// sorted keys. counts: 256 * sort_tiles(n) words of scratch.
+constexpr int SORT_TILE = 8192;
+inline size_t sort_tiles(size_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
+hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int end_bit, uint32_t* counts, uint64_t** result,
                           hipStream_t s);
 
 }  // namespace kls

@@ -1448,8 +1448,8 @@ __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Wide top-k (k above 64, up to no limit; src/sampler.cpp:42-51): keys of every logit, one device-wide sort,
-// then the tail over the sorted keys.
+// Wide top-k (k above what the mid path holds, up to no limit; src/sampler.cpp:42-51): keys of every logit, one
+// device-wide radix sort (kls_sort.hip), then the tail over the sorted keys.
 
 constexpr int WIDE_WG = 256;
 constexpr int WIDE_SEG = 4096;  // ids per keys workgroup (32-bit history counts: 16 KB of LDS)
@@ -2356,14 +2356,14 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
     int rb = 0;
     while ((1 << rb) < a.n_rows) ++rb;
     const size_t n = (size_t) a.n_rows * a.V;
-    size_t need = 0;
-    e = sort_keys_desc(nullptr, &need, w.keys, w.sorted, n, 32 + w.id_bits + rb, s);  // (a size query)
+    uint64_t* sorted = nullptr;
+    e = sort_keys_desc(w.keys, w.sorted, n, 32 + w.id_bits + rb, w.counts, &sorted, s);
     if (e != hipSuccess) return e;
-    if (need > w.sort_tmp_bytes) return hipErrorInvalidValue;
-    size_t bytes = w.sort_tmp_bytes;
-    e = sort_keys_desc(w.sort_tmp, &bytes, w.keys, w.sorted, n, 32 + w.id_bits + rb, s);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(TAIL_WG), 0, s, a, w);
+    // the tail reads the sorted buffer and keeps its terms in the other one
+    WideArgs t = w;
+    t.sorted = sorted;
+    t.keys = sorted == w.keys ? w.sorted : w.keys;
+    hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(TAIL_WG), 0, s, a, t);
     return hipGetLastError();
 }
 

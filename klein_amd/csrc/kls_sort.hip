@@ -1,13 +1,149 @@
-// Device-wide descending sort of 64-bit keys for the wide top-k path (rocPRIM's LSD radix sort).
-#include <rocprim/device/device_radix_sort.hpp>
-
+// Device-wide descending sort of 64-bit keys for the wide top-k path: a stable least-significant-digit radix sort,
+// 8 bits per pass, three kernels per pass (no memset, so a pass can be captured in a graph):
+//   1. sort_hist_kernel: each tile of SORT_TILE keys counts its digits in LDS, written digit-major:
+//      counts[digit * tiles + tile];
+//   2. sort_scan_kernel: one workgroup turns the counts into an exclusive scan in place (digit-major order, so
+//      digit d of tile t starts after every smaller digit and after digit d of every earlier tile);
+//   3. sort_scatter_kernel: each tile ranks its keys stably and writes them to their slots.
+// Descending order is ascending order of the inverted digit (255 - digit). Within a tile, key i of the tile is
+// held by wave i / 512, slot (i / 64) % 8, lane i % 64; a wave ranks its 512 keys slot by slot: the lanes of a
+// slot whose digits are equal are found with eight ballots, a key's rank is the wave's count of that digit so far
+// plus the equal lanes below it, and the lowest of those lanes adds the group's size to the wave's count (the
+// wave's LDS operations run in order). Then an exclusive prefix over the waves per digit gives every key its
+// place: tile base of its digit + earlier waves' count + its rank in the wave.
 #include "kls_internal.h"
 
 namespace kls {
+namespace {
 
-hipError_t sort_keys_desc(void* tmp, size_t* bytes, const uint64_t* in, uint64_t* out, size_t n, int end_bit,
+constexpr int ST_WG = 1024, ST_NW = ST_WG / 64, ST_PER = SORT_TILE / ST_WG;
+static_assert(ST_PER * 64 * ST_NW == SORT_TILE && ST_PER == 8, "tile layout");
+
+__device__ __forceinline__ uint32_t rdigit(uint64_t k, int shift) { return 255u - (uint32_t) ((k >> shift) & 255u); }
+
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+// Index of key s of this thread in its tile (wave-major: each wave holds 512 consecutive keys).
+__device__ __forceinline__ size_t tile_index(unsigned tile, int wave, int s, int lane) {
+    return (size_t) tile * SORT_TILE + (size_t) wave * 512 + (size_t) s * 64 + lane;
+}
+
+__global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __restrict__ in, uint32_t n, int shift,
+                                                          uint32_t tiles, uint32_t* __restrict__ counts) {
+    __shared__ uint32_t h[256];
+    const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < 256) h[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < ST_PER; ++s) {
+        const size_t i = tile_index(blockIdx.x, wave, s, lane);
+        if (i < n) atomicAdd(&h[rdigit(in[i], shift)], 1u);
+    }
+    __syncthreads();
+    if (tid < 256) counts[(size_t) tid * tiles + blockIdx.x] = h[tid];
+}
+
+// Exclusive scan of counts[0..m) in place, one workgroup: thread t takes a contiguous run of ceil(m / ST_WG).
+__global__ __launch_bounds__(ST_WG) void sort_scan_kernel(uint32_t* __restrict__ counts, uint32_t m) {
+    __shared__ uint32_t ws[ST_NW];
+    const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t c = (m + ST_WG - 1) / ST_WG;
+    const uint32_t lo = min(m, (uint32_t) tid * c), hi = min(m, lo + c);
+    uint32_t sum = 0u;
+    for (uint32_t i = lo; i < hi; ++i) sum += counts[i];
+    uint32_t x = sum;  // inclusive scan across the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = (uint32_t) __shfl_up((int) x, (unsigned) d, 64);
+        x += lane >= d ? y : 0u;
+    }
+    if (lane == 63) ws[wave] = x;
+    __syncthreads();
+    uint32_t run = x - sum;
+#pragma unroll
+    for (int w = 0; w < ST_NW; ++w) run += w < wave ? ws[w] : 0u;
+    for (uint32_t i = lo; i < hi; ++i) {
+        const uint32_t v = counts[i];
+        counts[i] = run;
+        run += v;
+    }
+}
+
+__global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
+                                                             uint32_t n, int shift, uint32_t tiles,
+                                                             const uint32_t* __restrict__ offs) {
+    __shared__ uint32_t cw[ST_NW][256];  // per wave: digit counts so far, then the earlier waves' counts
+    __shared__ uint32_t tb[256];         // this tile's first slot per digit
+    const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < ST_NW * 256; i += ST_WG) (&cw[0][0])[i] = 0u;
+    if (tid < 256) tb[tid] = offs[(size_t) tid * tiles + blockIdx.x];
+    uint64_t k[ST_PER];
+#pragma unroll
+    for (int s = 0; s < ST_PER; ++s) {
+        const size_t i = tile_index(blockIdx.x, wave, s, lane);
+        k[s] = i < n ? in[i] : 0ull;
+    }
+    __syncthreads();
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t rk[ST_PER];
+#pragma unroll
+    for (int s = 0; s < ST_PER; ++s) {
+        const bool valid = tile_index(blockIdx.x, wave, s, lane) < n;
+        const uint32_t d = rdigit(k[s], shift);
+        uint64_t same = ballot64(valid);  // (all lanes take part in every ballot)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (d >> b) & 1u;
+            const uint64_t m = ballot64(bit);
+            same &= bit ? m : ~m;
+        }
+        const uint32_t before = (uint32_t) __popcll(same & below);
+        const uint32_t prev = cw[wave][d];
+        rk[s] = prev + before;
+        if (valid && before == 0u) cw[wave][d] = prev + (uint32_t) __popcll(same);
+    }
+    __syncthreads();
+    if (tid < 256) {
+        uint32_t run = 0u;
+#pragma unroll
+        for (int w = 0; w < ST_NW; ++w) {
+            const uint32_t v = cw[w][tid];
+            cw[w][tid] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < ST_PER; ++s) {
+        if (tile_index(blockIdx.x, wave, s, lane) < n) {
+            const uint32_t d = rdigit(k[s], shift);
+            const uint32_t pos = tb[d] + cw[wave][d] + rk[s];
+            if (pos < n) out[pos] = k[s];  // (always: the counts are the tile's own)
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int end_bit, uint32_t* counts, uint64_t** result,
                           hipStream_t s) {
-    return rocprim::radix_sort_keys_desc(tmp, *bytes, in, out, n, 0u, (unsigned) end_bit, s);
+    if (n == 0 || n >= (1ull << 32) || end_bit < 1 || end_bit > 64) return hipErrorInvalidValue;
+    const uint32_t tiles = (uint32_t) sort_tiles(n);
+    uint64_t* src = a;
+    uint64_t* dst = b;
+    for (int shift = 0; shift < end_bit; shift += 8) {
+        hipLaunchKernelGGL(sort_hist_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, (uint32_t) n, shift, tiles, counts);
+        hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(ST_WG), 0, s, counts, 256u * tiles);
+        hipLaunchKernelGGL(sort_scatter_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, dst, (uint32_t) n, shift, tiles,
+                           counts);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        uint64_t* t = src;
+        src = dst;
+        dst = t;
+    }
+    *result = src;
+    return hipSuccess;
 }
 
 }  // namespace kls

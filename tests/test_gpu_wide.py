@@ -179,3 +179,58 @@ def test_wide_sample_and_verify_with_history(torch_cuda, K, oracle_lib, k):
         ot, oa, counts = O.verify(x, drafts, p, u, counts, O.MODE_TOTAL)
         assert acc == oa and list(toks) == list(ot[:oa + 1]), (step, acc, oa)
     S.close()
+
+
+@pytest.mark.parametrize("V", [8192, 8193, 16385])
+def test_wide_sort_tile_edges(torch_cuda, K, oracle_lib, V):
+    """The radix sort at tile boundaries (8,192 keys a tile: exactly one, one past, two and one past), on rows with
+    all-equal runs (keys that differ in the id bits only) and a row without a limit."""
+    torch = torch_cuda
+    O = oracle_lib
+    rng = np.random.default_rng(V)
+    x = head_rows(rng, 1, V)
+    x[0, ::3] = np.float32(1.25)
+    p = W.Params(temperature=1.0, top_k=0, top_p=0.9)
+    u = rng.random(1)
+    S = K.Sampler(p, n_vocab=V, max_rows=1)
+    assert S.path == "wide"
+    out = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    say("sort tile edges", V)
+    S.sample_batch(dev(torch, x), dev(torch, u), out)
+    torch.cuda.synchronize()
+    t = check_row(S, O, x[0], p, u[0], None, 0, f"V{V}")
+    assert int(out.cpu()[0]) == t
+    S.close()
+
+
+def test_wide_verify_steps_captured(torch_cuda, K, oracle_lib):
+    """Verify steps without a top-k limit are one graph launch like the others (keys, the sort's passes and the
+    tail captured together): five steps against the oracle, then the graph timed by its hook."""
+    import ctypes as C
+    from klein_amd import _lib
+    O = oracle_lib
+    torch = torch_cuda
+    V = 70001
+    rng = np.random.default_rng(88)
+    p = W.Params(temperature=0.8, top_k=0, top_p=0.9, seed=4)
+    nb = 4
+    S = K.Sampler(p, n_vocab=V, max_rows=nb)
+    assert S.path == "wide"
+    x = dev(torch, head_rows(rng, nb, V))
+    xh = x.cpu().numpy()
+    counts = np.zeros(V, np.int32)
+    for step in range(5):
+        u = rng.random(nb)
+        m = step % nb
+        drafts = rng.integers(0, V, nb - 1).astype(np.int32)
+        for i in range(m):
+            drafts[i] = O.sample(xh[i], p, u[i], counts, O.MODE_TOTAL)[0]
+        say("wide verify (captured)", step)
+        toks, acc = S.verify(x, drafts, u=u)
+        ot, oa, _ = O.verify(xh, drafts, p, u, counts, O.MODE_TOTAL)
+        assert acc == oa and list(toks) == list(ot[:oa + 1]), (step, acc, oa)
+    us = C.c_double()
+    _lib.check(_lib.lib().kls_debug_time_verify(S._h, 2, 2, None, C.byref(us)), "kls_debug_time_verify")
+    assert us.value > 0.0
+    S.close()
