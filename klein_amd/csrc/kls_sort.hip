@@ -43,14 +43,27 @@ __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __rest
     if (tid < 256) counts[(size_t) tid * tiles + blockIdx.x] = h[tid];
 }
 
-// Exclusive scan of counts[0..m) in place, one workgroup: thread t takes a contiguous run of ceil(m / ST_WG).
+// Exclusive scan of counts[0..m) in place, one workgroup: thread t takes a contiguous run of c = ceil(m / ST_WG)
+// entries. Runs of up to SCAN_REG entries are loaded into registers at once (every load in flight together);
+// longer ones (grids of more than 128 tiles) are read twice in loops.
+constexpr int SCAN_REG = 32;
+
 __global__ __launch_bounds__(ST_WG) void sort_scan_kernel(uint32_t* __restrict__ counts, uint32_t m) {
     __shared__ uint32_t ws[ST_NW];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t c = (m + ST_WG - 1) / ST_WG;
     const uint32_t lo = min(m, (uint32_t) tid * c), hi = min(m, lo + c);
+    const bool reg = c <= SCAN_REG;  // (uniform)
+    uint32_t v[SCAN_REG];
     uint32_t sum = 0u;
-    for (uint32_t i = lo; i < hi; ++i) sum += counts[i];
+    if (reg) {
+#pragma unroll
+        for (int j = 0; j < SCAN_REG; ++j) v[j] = lo + j < hi ? counts[lo + j] : 0u;
+#pragma unroll
+        for (int j = 0; j < SCAN_REG; ++j) sum += v[j];
+    } else {
+        for (uint32_t i = lo; i < hi; ++i) sum += counts[i];
+    }
     uint32_t x = sum;  // inclusive scan across the wave
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -62,10 +75,18 @@ __global__ __launch_bounds__(ST_WG) void sort_scan_kernel(uint32_t* __restrict__
     uint32_t run = x - sum;
 #pragma unroll
     for (int w = 0; w < ST_NW; ++w) run += w < wave ? ws[w] : 0u;
-    for (uint32_t i = lo; i < hi; ++i) {
-        const uint32_t v = counts[i];
-        counts[i] = run;
-        run += v;
+    if (reg) {
+#pragma unroll
+        for (int j = 0; j < SCAN_REG; ++j) {
+            if (lo + j < hi) counts[lo + j] = run;
+            run += v[j];
+        }
+    } else {
+        for (uint32_t i = lo; i < hi; ++i) {
+            const uint32_t y = counts[i];
+            counts[i] = run;
+            run += y;
+        }
     }
 }
 
