@@ -205,12 +205,12 @@ int wide_id_bits(int V);  // key bits the ids of a V-entry vocabulary take
 hipError_t launch_mid(const RowsArgs& a, const MidArgs& m, bool penalize, hipStream_t s);
 hipError_t prepare_mid_kernels();  // once per device: LDS limit of the kernel with a count table
 
-// Descending device-wide sort of n 64-bit keys (n < 2^32) on bits [0, end_bit) (kls_sort.hip): a stable radix
-// sort, 8 bits per pass, alternating between the buffers a (the input) and b; *result is the one that holds the
-// sorted keys. counts: 256 * sort_tiles(n) words of scratch.
+// Descending device-wide sort of n 64-bit keys (n < 2^32) on bits [begin_bit, end_bit) (kls_sort.hip): a stable
+// radix sort, 8 bits per pass, alternating between the buffers a (the input) and b; *result is the one that holds
+// the sorted keys. Keys equal on those bits keep their input order. counts: 256 * sort_tiles(n) words of scratch.
 constexpr int SORT_TILE = 8192;
 inline size_t sort_tiles(size_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
-hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int end_bit, uint32_t* counts, uint64_t** result,
-                          hipStream_t s);
+hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int begin_bit, int end_bit, uint32_t* counts,
+                          uint64_t** result, hipStream_t s);
 
 }  // namespace kls

@@ -1503,12 +1503,18 @@ __shared__ int s_wide_n;  // kk, then the min-p length
 // whose exact sum could leave the binade (A + f < 2^52, or A + f >= 2^53 - 1, or t/u huge) is added with the real
 // double addition instead, and the scan restarts after it in the new binade; so is every term while acc is 0 or
 // subnormal. Identical results to the sequential loop, in ~31 workgroup steps for 248,320 terms.
+// Increments are integers held in doubles: while no term leaves the binade every increment and every partial
+// count is below 2^53 in magnitude, so the double arithmetic on them is exact (and full rate, with no integer
+// conversions); past a term that leaves the binade the values are discarded anyway.
 struct ParMap {
-    long long d0, d1;  // increments (in units of u) for incoming parity 0 / 1
-    uint32_t p;        // bit 0: parity after, from parity 0; bit 1: from parity 1
+    double d0, d1;  // increments (in units of u) for incoming parity 0 / 1
+    uint32_t p;     // bit 0: parity after, from parity 0; bit 1: from parity 1
 };
 
-__device__ __forceinline__ ParMap par_identity() { return ParMap{0, 0, 2u}; }
+__device__ __forceinline__ ParMap par_identity() { return ParMap{0.0, 0.0, 2u}; }
+
+// Parity of an integer-valued double below 2^53 in magnitude (0 or 1).
+__device__ __forceinline__ uint32_t dparity(double x) { return (uint32_t) (x - 2.0 * floor(0.5 * x)); }
 
 // e first, then l
 __device__ __forceinline__ ParMap par_compose(const ParMap& e, const ParMap& l) {
@@ -1523,15 +1529,16 @@ __device__ __forceinline__ ParMap par_compose(const ParMap& e, const ParMap& l) 
 // A map moved across lanes by DPP control CTRL (rows ROWS enabled); lanes with no source (or a disabled row)
 // get the identity map.
 template <int CTRL, int ROWS>
-__device__ __forceinline__ long long dpp_ll0(long long v) {
-    const uint32_t lo = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) (unsigned long long) v, CTRL, ROWS, 0xf, false);
-    const uint32_t hi = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) ((unsigned long long) v >> 32), CTRL, ROWS, 0xf, false);
-    return (long long) (((unsigned long long) hi << 32) | lo);
+__device__ __forceinline__ double dpp_d0(double x) {
+    const uint64_t v = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) v, CTRL, ROWS, 0xf, false);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) (v >> 32), CTRL, ROWS, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);  // (0.0 where there is no source)
 }
 
 template <int CTRL, int ROWS>
 __device__ __forceinline__ ParMap dpp_map(const ParMap& m) {
-    return ParMap{dpp_ll0<CTRL, ROWS>(m.d0), dpp_ll0<CTRL, ROWS>(m.d1),
+    return ParMap{dpp_d0<CTRL, ROWS>(m.d0), dpp_d0<CTRL, ROWS>(m.d1),
                   (uint32_t) __builtin_amdgcn_update_dpp(2, (int) m.p, CTRL, ROWS, 0xf, false)};
 }
 
@@ -1551,8 +1558,7 @@ __device__ __forceinline__ ParMap wave_scan_map(ParMap x) {
 }
 
 __device__ __forceinline__ ParMap rdlane_map(const ParMap& m, int l) {
-    return ParMap{(long long) rdlane64((uint64_t) m.d0, l), (long long) rdlane64((uint64_t) m.d1, l),
-                  (uint32_t) __builtin_amdgcn_readlane((int) m.p, l)};
+    return ParMap{rdlaned(m.d0, l), rdlaned(m.d1, l), (uint32_t) __builtin_amdgcn_readlane((int) m.p, l)};
 }
 
 __shared__ ParMap s_rp_wave[TAIL_WG / 64];
@@ -1560,28 +1566,30 @@ __shared__ int s_rp_first;
 __shared__ double s_rp_acc;
 __shared__ int s_rp_next, s_rp_stop;
 
-// The map of one term t in the binade of 2^E (f: its integer part in units of u; cross: too large to map).
-__device__ __forceinline__ ParMap term_map(double t, int E, long long* f, bool* cross) {
+// The map of one term t in the binade of 2^E (f: its integer part in units of u; cross: too large to map: any
+// |t/u| >= 2^53 takes the sum out of the binade).
+__device__ __forceinline__ ParMap term_map(double t, int E, double* f, bool* cross) {
     const double q = ldexp(t, 52 - E);
     ParMap m = par_identity();
-    *f = 0;
+    *f = 0.0;
     *cross = false;
-    if (!(fabs(q) < 0x1p62)) {
+    if (!(fabs(q) < 0x1p53)) {
         *cross = true;  // (handled by the real addition; the map is not used past it)
         return m;
     }
     const double fl = floor(q);
-    const long long fi = (long long) fl;
-    *f = fi;
+    *f = fl;
     const double ph = q - fl;  // exact
+    const uint32_t pf = dparity(fl);
     if (ph == 0.5) {
-        m.d0 = fi + (fi & 1);
-        m.d1 = fi + ((fi + 1) & 1);
+        m.d0 = fl + (double) pf;          // (A + d even from either parity)
+        m.d1 = fl + (double) (1u - pf);
         m.p = 0u;
     } else {
-        const long long d = fi + (ph > 0.5 ? 1 : 0);
+        const double d = fl + (ph > 0.5 ? 1.0 : 0.0);
+        const uint32_t pd = ph > 0.5 ? 1u - pf : pf;
         m.d0 = m.d1 = d;
-        m.p = (uint32_t) (d & 1) | ((uint32_t) ((d + 1) & 1) << 1);
+        m.p = pd | ((1u - pd) << 1);
     }
     return m;
 }
@@ -1589,20 +1597,21 @@ __device__ __forceinline__ ParMap term_map(double t, int E, long long* f, bool* 
 // Replays the chain over t[0..n) from `acc` with the whole workgroup (every thread calls it, uniformly);
 // stop(acc, i) is evaluated on each partial result after term i, and the first i for which it holds ends the
 // chain (returned in *stopped, else -1). Returns the last partial result.
-// RP_PT terms per thread in one block: thread tid takes RP_PT consecutive terms, composes their maps in
-// registers, and the workgroup scans the threads' maps, so a block covers TAIL_WG * RP_PT terms with one scan and
-// two barriers; each thread then walks its own terms from the scanned prefix to find the first that leaves the
-// binade or meets the stop (the terms are read again rather than held). 8 suits long chains (a pass is bound by
-// one CU's VALU time, the scans and barriers amortized), 1 chains of at most TAIL_WG terms (no serial walk).
-template <int RP_PT, typename F>
+// RP_PT terms per thread in one block: thread tid loads RP_PT consecutive terms into registers (the loads issued
+// together, so a block waits for one memory latency, not one per term), composes their maps, and the workgroup
+// scans the threads' maps, so a block covers TAIL_WG * RP_PT terms with one scan and two barriers; each thread
+// then walks its own terms from the scanned prefix to find the first that leaves the binade or meets the stop.
+// 8 suits long chains (the scans and barriers amortized), 1 chains of at most TAIL_WG terms (no serial walk).
+// NEG: the chain adds -t_i (the draw's subtractions) instead of t_i.
+template <int RP_PT, bool NEG = false, typename F>
 __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F stop, int* stopped) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr long long TWO52 = 1ll << 52, TWO53 = 1ll << 53;
+    constexpr double TWO52 = 0x1p52, TWO53 = 0x1p53;
     int i = 0, st = -1;
     while (i < n) {
         if (!(acc >= 0x1p-1000 && acc <= 0x1.fffffffffffffp+1023)) {
             // zero, negative, subnormal, tiny, infinite or NaN: one real addition (every thread the same)
-            acc = __dadd_rn(acc, t[i]);
+            acc = __dadd_rn(acc, NEG ? -t[i] : t[i]);
             if (stop(acc, i)) {
                 st = i;
                 break;
@@ -1614,18 +1623,20 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
         (void) frexp(acc, &E);  // acc in [2^(E-1), 2^E)
         E -= 1;
         const double u = ldexp(1.0, E - 52);
-        const long long A0 = (long long) ldexp(acc, 52 - E);
-        const uint32_t pi0 = (uint32_t) (A0 & 1);
+        const double A0 = ldexp(acc, 52 - E);  // (an integer in [2^52, 2^53))
+        const uint32_t pi0 = dparity(A0);
         const int j0 = i + tid * RP_PT;
+        double tv[RP_PT];  // this thread's terms (addresses clamped to the chain; terms past it are not used)
+#pragma unroll
+        for (int q = 0; q < RP_PT; ++q) tv[q] = NEG ? -t[min(j0 + q, n - 1)] : t[min(j0 + q, n - 1)];
         // the composed map of this thread's terms
         ParMap M = par_identity();
 #pragma unroll
         for (int q = 0; q < RP_PT; ++q) {
-            if (j0 + q < n) {
-                long long f;
-                bool c;
-                M = par_compose(M, term_map(t[j0 + q], E, &f, &c));
-            }
+            double f;
+            bool c;
+            const ParMap m = term_map(tv[q], E, &f, &c);
+            if (j0 + q < n) M = par_compose(M, m);
         }
         // workgroup scan of the threads' maps: each wave's (DPP; a wave past the terms holds identities and
         // skips it), then the waves' totals (a 16-lane DPP scan that every wave runs on the totals it reads back)
@@ -1644,35 +1655,37 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
         ParMap X = par_compose(pre, xe);
         int hq = -1;
         bool h_cross = false;
-        long long h_A = 0;
-        double h_t = 0.0, h_nxt = 0.0;
-        for (int q = 0; q < RP_PT && j0 + q < n; ++q) {
+        double h_A = 0.0, h_t = 0.0, h_nxt = 0.0;
+#pragma unroll
+        for (int q = 0; q < RP_PT; ++q) {
             const int j = j0 + q;
-            const double tj = t[j];
-            long long f;
-            bool cross;
-            const ParMap m = term_map(tj, E, &f, &cross);
-            const long long Aj = A0 + (pi0 ? X.d1 : X.d0);
-            const uint32_t pij = pi0 ? ((X.p >> 1) & 1u) : (X.p & 1u);
-            const long long dj = pij ? m.d1 : m.d0;
-            if (!cross) cross = (Aj + f < TWO52) || (Aj + f >= TWO53 - 1);
-            const double nxt = (double) (Aj + dj) * u;  // (exact when no earlier term crossed)
-            if (cross || stop(nxt, j)) {
-                hq = q;
-                h_cross = cross;
-                h_A = Aj;
-                h_t = tj;
-                h_nxt = nxt;
-                break;
+            if (hq < 0 && j < n) {
+                const double tj = tv[q];
+                double f;
+                bool cross;
+                const ParMap m = term_map(tj, E, &f, &cross);
+                const double Aj = A0 + (pi0 ? X.d1 : X.d0);
+                const uint32_t pij = pi0 ? ((X.p >> 1) & 1u) : (X.p & 1u);
+                const double dj = pij ? m.d1 : m.d0;
+                if (!cross) cross = (Aj + f < TWO52) || (Aj + f >= TWO53 - 1.0);
+                const double nxt = (Aj + dj) * u;  // (exact when no earlier term crossed)
+                if (cross || stop(nxt, j)) {
+                    hq = q;
+                    h_cross = cross;
+                    h_A = Aj;
+                    h_t = tj;
+                    h_nxt = nxt;
+                } else {
+                    X = par_compose(X, m);
+                }
             }
-            X = par_compose(X, m);
         }
         if (hq >= 0) atomicMin(&s_rp_first, j0 + hq - i);
         __syncthreads();
         const int first = s_rp_first;
         if (first == 0x7fffffff) {
             // no term left the binade or stopped: the block's total
-            acc = (double) (A0 + (pi0 ? tot_all.d1 : tot_all.d0)) * u;
+            acc = (A0 + (pi0 ? tot_all.d1 : tot_all.d0)) * u;
             i += TAIL_WG * RP_PT;
         } else {
             if (hq >= 0 && j0 + hq - i == first) {
@@ -1681,7 +1694,7 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
                 double r;
                 int s2 = -1;
                 if (h_cross) {
-                    r = __dadd_rn((double) h_A * u, h_t);
+                    r = __dadd_rn(h_A * u, h_t);
                     if (stop(r, j)) s2 = j;
                 } else {
                     r = h_nxt;
@@ -1839,6 +1852,47 @@ struct FastKeyFmt {
     __device__ int id(uint64_t k) const { return (int) ~(uint32_t) k; }
 };
 
+// Passes of the tail over its candidates, TU per thread per round with their loads issued together (one memory
+// latency per round). tail_terms: t[i] = e_i (:55-58) for i < k, and s_wide_n lowered to the first NaN key;
+// i = b + lane + q * TAIL_WG with rounds uniform in the wave (expf_glibc_tab reads across lanes).
+template <int TU, typename Fmt>
+__device__ __forceinline__ void tail_terms(const uint64_t* K, int k, double* t, float maxl, float temp, const Fmt& fmt,
+                                           uint64_t etab, int lane, int wave) {
+    for (int b = wave * 64; b < k; b += TAIL_WG * TU) {
+        uint32_t o[TU];
+#pragma unroll
+        for (int q = 0; q < TU; ++q) o[q] = fmt.img(K[min(b + lane + q * TAIL_WG, k - 1)]);
+#pragma unroll
+        for (int q = 0; q < TU; ++q) {
+            const int i = b + lane + q * TAIL_WG;
+            const float e = expf_glibc_tab(__fdiv_rn(__fsub_rn(unord_f32(o[q]), maxl), temp), etab);
+            if (i < k) {
+                if (o[q] == 0u) atomicMin(&s_wide_n, i);
+                t[i] = (double) e;
+            }
+        }
+    }
+}
+// tail_probs: t[i] = p_i = (float) (e_i / sum) (:60) for i < kk, and s_wide_n lowered to the first i >= 1 with
+// p_i < thr (min-p, :62-68).
+template <int TU>
+__device__ __forceinline__ void tail_probs(double* t, int kk, double sum, float thr, float min_p, int tid) {
+    for (int b = tid; b < kk; b += TAIL_WG * TU) {
+        double e[TU];
+#pragma unroll
+        for (int q = 0; q < TU; ++q) e[q] = t[min(b + q * TAIL_WG, kk - 1)];
+#pragma unroll
+        for (int q = 0; q < TU; ++q) {
+            const int i = b + q * TAIL_WG;
+            if (i < kk) {
+                const float pi = __double2float_rn(__ddiv_rn(e[q], sum));
+                if (min_p > 0.0f && i >= 1 && !(pi >= thr)) atomicMin(&s_wide_n, i);
+                t[i] = (double) pi;
+            }
+        }
+    }
+}
+
 // The tail of src/sampler.cpp:53-88 over a row's sorted keys K (value descending, id ascending; the first k are
 // the candidates, ended early by the first key of value image 0, a NaN), with the whole workgroup (TAIL_WG
 // threads, uniform control flow): the per-candidate terms (e_i, then p_i) go to t[0..k) as doubles, and every sum
@@ -1867,13 +1921,13 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
     }
     const float maxl = unord_f32(o0);
     // e_i (:55-58) of every candidate, and kk: the first NaN key ends the candidates
+    const uint64_t etab = kExp2Tab[lane & 31];
     if (tid == 0) s_wide_n = k;
     __syncthreads();
-    for (int i = tid; i < k; i += TAIL_WG) {
-        const uint32_t o = fmt.img(K[i]);
-        if (o == 0u) atomicMin(&s_wide_n, i);
-        t[i] = (double) expf_glibc(__fdiv_rn(__fsub_rn(unord_f32(o), maxl), p.temperature));
-    }
+    if (k > TAIL_WG)
+        tail_terms<8>(K, k, t, maxl, p.temperature, fmt, etab, lane, wave);
+    else
+        tail_terms<1>(K, k, t, maxl, p.temperature, fmt, etab, lane, wave);
     __syncthreads();
     const int kk = s_wide_n;
     int n = 0;
@@ -1890,11 +1944,10 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
         const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
         if (tid == 0) s_wide_n = kk;
         __syncthreads();
-        for (int i = tid; i < kk; i += TAIL_WG) {
-            const float pi = __double2float_rn(__ddiv_rn(t[i], sum));
-            if (p.min_p > 0.0f && i >= 1 && !(pi >= thr)) atomicMin(&s_wide_n, i);
-            t[i] = (double) pi;
-        }
+        if (kk > TAIL_WG)
+            tail_probs<8>(t, kk, sum, thr, p.min_p, tid);
+        else
+            tail_probs<1>(t, kk, sum, thr, p.min_p, tid);
         __syncthreads();
         n = s_wide_n;
         dbg_p = act ? (float) t[lane] : 0.0f;
@@ -1912,14 +1965,11 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
         // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a
         // chain of additions of -p_i (exactly the subtractions)
         const double r0 = __dadd_rn(__dmul_rn(cin.u, __dsub_rn(total, 0.0)), 0.0);
-        __syncthreads();  // (every thread has read its p_i for the debug copy)
-        for (int i = tid; i < n; i += TAIL_WG) t[i] = -t[i];  // (p_i negated in place for the chain)
-        __syncthreads();
         const auto spent = [](double r, int) { return r <= 0.0; };
         if (n > TAIL_WG)
-            replay_sum<8>(t, n, r0, spent, &st);
+            replay_sum<8, true>(t, n, r0, spent, &st);
         else
-            replay_sum<1>(t, n, r0, spent, &st);
+            replay_sum<1, true>(t, n, r0, spent, &st);
         idx = st >= 0 ? st : n - 1;
     }
     if (wave != 0) return;
@@ -2357,7 +2407,9 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
     while ((1 << rb) < a.n_rows) ++rb;
     const size_t n = (size_t) a.n_rows * a.V;
     uint64_t* sorted = nullptr;
-    e = sort_keys_desc(w.keys, w.sorted, n, 32 + w.id_bits + rb, w.counts, &sorted, s);
+    // The keys are written in (row, id) order and the sort is stable, so sorting on the row and value fields
+    // alone leaves equal values in ascending id order, as the id field would: its passes are skipped.
+    e = sort_keys_desc(w.keys, w.sorted, n, w.id_bits, 32 + w.id_bits + rb, w.counts, &sorted, s);
     if (e != hipSuccess) return e;
     // the tail reads the sorted buffer and keeps its terms in the other one
     WideArgs t = w;

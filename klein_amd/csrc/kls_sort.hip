@@ -146,13 +146,14 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
 
 }  // namespace
 
-hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int end_bit, uint32_t* counts, uint64_t** result,
-                          hipStream_t s) {
-    if (n == 0 || n >= (1ull << 32) || end_bit < 1 || end_bit > 64) return hipErrorInvalidValue;
+hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int begin_bit, int end_bit, uint32_t* counts,
+                          uint64_t** result, hipStream_t s) {
+    if (n == 0 || n >= (1ull << 32) || begin_bit < 0 || end_bit <= begin_bit || end_bit > 64)
+        return hipErrorInvalidValue;
     const uint32_t tiles = (uint32_t) sort_tiles(n);
     uint64_t* src = a;
     uint64_t* dst = b;
-    for (int shift = 0; shift < end_bit; shift += 8) {
+    for (int shift = begin_bit; shift < end_bit; shift += 8) {
         hipLaunchKernelGGL(sort_hist_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, (uint32_t) n, shift, tiles, counts);
         hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(ST_WG), 0, s, counts, 256u * tiles);
         hipLaunchKernelGGL(sort_scatter_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, dst, (uint32_t) n, shift, tiles,
