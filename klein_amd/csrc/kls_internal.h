@@ -48,6 +48,7 @@ struct ResultBlock {
 constexpr uint32_t FAULT_COUNT_WAIT = 1;   // the history count table was not announced complete in time
 constexpr uint32_t FAULT_BOUND_WAIT = 2;   // the early bound of a 16-wave segment was not published in time
 constexpr uint32_t FAULT_NARROW = 3;       // a mid top-k threshold bisection did not end (not reachable)
+constexpr uint32_t FAULT_WIDE_MAP = 4;     // a chunk map of the wide tail left its binade (not reachable)
 
 struct SamplingParams {
     float temperature;
@@ -125,12 +126,38 @@ constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 20;
 // with row field = n_rows - 1 - row, so one descending device-wide sort of all rows' keys leaves each row's keys
 // contiguous, value-descending and, on equal values, id-ascending (the fast path's order). NaN maps to the
 // value image 0, after every number. The sorted keys then go through the O(k) tail in reference order.
+// The wide path's tail cuts each of its double chains into chunks of WT_CHUNK terms (kls_kernels.hip):
+constexpr int WT_CHUNK = 2048;
+// a chunk's place in the chain being resolved: its terms composed to one parity map in the binade 2^E when
+// `mapped` (else it is replayed term by term)
+struct WideChunk {
+    double d0, d1;  // increments in units of 2^(E-52) from an incoming even / odd partial result
+    uint32_t p;     // parity after: bit 0 from even, bit 1 from odd
+    int32_t E;
+    int32_t mapped;
+    int32_t pad;
+};
+// a row's state between the tail's kernels
+struct WideRow {
+    int32_t kk;     // candidates: keys before the first NaN key
+    int32_t n_mp;   // kept by min-p
+    int32_t n_top;  // kept by top-p
+    int32_t pad;
+    double sum;     // softmax total
+    double total;   // the draw's total
+    double r0;      // the draw's start, u * total
+};
+
 struct WideArgs {
     uint64_t* keys;       // [n_rows * V]
     uint64_t* sorted;     // [n_rows * V] (the sort alternates between the two buffers)
     uint32_t* counts;     // the sort's digit counts: 256 * sort_tiles(max_rows * V)
     int32_t k;            // MID_KMAX < k <= V (or a k the mid path cannot hold)
     int32_t id_bits;      // ids are below 1 << id_bits
+    int32_t chunks;       // chunks per row: ceil(k / WT_CHUNK)
+    double* part;         // [max_rows * chunks] term sums of the chunks
+    WideChunk* chunk;     // [max_rows * chunks]
+    WideRow* rowst;       // [max_rows]
 };
 
 // Mid top-k (KCAP < k <= MID_KMAX; src/sampler.cpp:42-51), one kernel: 1024-thread workgroups over segments of

@@ -1601,7 +1601,8 @@ __device__ __forceinline__ ParMap term_map(double t, int E, double* f, bool* cro
 // together, so a block waits for one memory latency, not one per term), composes their maps, and the workgroup
 // scans the threads' maps, so a block covers TAIL_WG * RP_PT terms with one scan and two barriers; each thread
 // then walks its own terms from the scanned prefix to find the first that leaves the binade or meets the stop.
-// 8 suits long chains (the scans and barriers amortized), 1 chains of at most TAIL_WG terms (no serial walk).
+// 1 suits chains of at most TAIL_WG terms (no serial walk: the mid path's tail), 2 the wide tail's chunks of
+// 2 * TAIL_WG terms.
 // NEG: the chain adds -t_i (the draw's subtractions) instead of t_i.
 template <int RP_PT, bool NEG = false, typename F>
 __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F stop, int* stopped) {
@@ -1716,15 +1717,15 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
     return acc;
 }
 
-// Test hook: replay_sum over t[0..n) from acc0 (8 terms per thread above TAIL_WG terms, else 1, as the tail
-// chooses); mode 0 never stops, 1 stops at acc >= thr, 2 at acc <= 0.
+// Test hook: replay_sum over t[0..n) from acc0 (2 terms per thread above TAIL_WG terms, as the wide tail's
+// replayed chunks, else 1, as the mid path's tail); mode 0 never stops, 1 stops at acc >= thr, 2 at acc <= 0.
 // out[0] = the result, out[1] = the stop index (-1: none).
 __global__ __launch_bounds__(TAIL_WG) void sum_replay_kernel(const double* t, int n, double acc0, int mode, double thr,
                                                              double* out) {
     int st;
     const auto stop = [mode, thr](double acc, int) { return mode == 1 ? acc >= thr : mode == 2 ? acc <= 0.0 : false; };
-    // (the tail's choice of terms per thread)
-    const double r = n > TAIL_WG ? replay_sum<8>(t, n, acc0, stop, &st) : replay_sum<1>(t, n, acc0, stop, &st);
+    // (the tails' choices of terms per thread)
+    const double r = n > TAIL_WG ? replay_sum<2>(t, n, acc0, stop, &st) : replay_sum<1>(t, n, acc0, stop, &st);
     if (threadIdx.x == 0) {
         out[0] = r;
         out[1] = (double) st;
@@ -1852,52 +1853,11 @@ struct FastKeyFmt {
     __device__ int id(uint64_t k) const { return (int) ~(uint32_t) k; }
 };
 
-// Passes of the tail over its candidates, TU per thread per round with their loads issued together (one memory
-// latency per round). tail_terms: t[i] = e_i (:55-58) for i < k, and s_wide_n lowered to the first NaN key;
-// i = b + lane + q * TAIL_WG with rounds uniform in the wave (expf_glibc_tab reads across lanes).
-template <int TU, typename Fmt>
-__device__ __forceinline__ void tail_terms(const uint64_t* K, int k, double* t, float maxl, float temp, const Fmt& fmt,
-                                           uint64_t etab, int lane, int wave) {
-    for (int b = wave * 64; b < k; b += TAIL_WG * TU) {
-        uint32_t o[TU];
-#pragma unroll
-        for (int q = 0; q < TU; ++q) o[q] = fmt.img(K[min(b + lane + q * TAIL_WG, k - 1)]);
-#pragma unroll
-        for (int q = 0; q < TU; ++q) {
-            const int i = b + lane + q * TAIL_WG;
-            const float e = expf_glibc_tab(__fdiv_rn(__fsub_rn(unord_f32(o[q]), maxl), temp), etab);
-            if (i < k) {
-                if (o[q] == 0u) atomicMin(&s_wide_n, i);
-                t[i] = (double) e;
-            }
-        }
-    }
-}
-// tail_probs: t[i] = p_i = (float) (e_i / sum) (:60) for i < kk, and s_wide_n lowered to the first i >= 1 with
-// p_i < thr (min-p, :62-68).
-template <int TU>
-__device__ __forceinline__ void tail_probs(double* t, int kk, double sum, float thr, float min_p, int tid) {
-    for (int b = tid; b < kk; b += TAIL_WG * TU) {
-        double e[TU];
-#pragma unroll
-        for (int q = 0; q < TU; ++q) e[q] = t[min(b + q * TAIL_WG, kk - 1)];
-#pragma unroll
-        for (int q = 0; q < TU; ++q) {
-            const int i = b + q * TAIL_WG;
-            if (i < kk) {
-                const float pi = __double2float_rn(__ddiv_rn(e[q], sum));
-                if (min_p > 0.0f && i >= 1 && !(pi >= thr)) atomicMin(&s_wide_n, i);
-                t[i] = (double) pi;
-            }
-        }
-    }
-}
-
-// The tail of src/sampler.cpp:53-88 over a row's sorted keys K (value descending, id ascending; the first k are
-// the candidates, ended early by the first key of value image 0, a NaN), with the whole workgroup (TAIL_WG
-// threads, uniform control flow): the per-candidate terms (e_i, then p_i) go to t[0..k) as doubles, and every sum
-// is the reference's sequential double chain: tail_exact when at most TAIL_WG candidates meet the exactness
-// condition above, else replayed exactly (replay_sum). Publishes the row's token.
+// The tail of src/sampler.cpp:53-88 over a row's sorted keys K (value descending, id ascending; the first
+// k <= TAIL_WG are the candidates, ended early by the first key of value image 0, a NaN), with the whole
+// workgroup (TAIL_WG threads, one candidate each, uniform control flow): the per-candidate terms (e_i, then p_i)
+// go to t[0..k) as doubles, and every sum is the reference's sequential double chain: tail_exact when the
+// candidates meet the exactness condition above, else replayed exactly (replay_sum). Publishes the row's token.
 template <typename Fmt>
 __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k, double* t, const CallIn& cin,
                             const Fmt& fmt) {
@@ -1921,33 +1881,37 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
     }
     const float maxl = unord_f32(o0);
     // e_i (:55-58) of every candidate, and kk: the first NaN key ends the candidates
-    const uint64_t etab = kExp2Tab[lane & 31];
     if (tid == 0) s_wide_n = k;
     __syncthreads();
-    if (k > TAIL_WG)
-        tail_terms<8>(K, k, t, maxl, p.temperature, fmt, etab, lane, wave);
-    else
-        tail_terms<1>(K, k, t, maxl, p.temperature, fmt, etab, lane, wave);
+    {
+        const uint32_t o = fmt.img(K[min(tid, k - 1)]);
+        const float e = expf_glibc_tab(__fdiv_rn(__fsub_rn(unord_f32(o), maxl), p.temperature), kExp2Tab[lane & 31]);
+        if (tid < k) {
+            if (o == 0u) atomicMin(&s_wide_n, tid);
+            t[tid] = (double) e;
+        }
+    }
     __syncthreads();
     const int kk = s_wide_n;
     int n = 0;
     float dbg_p = 0.0f;
-    int idx = kk <= TAIL_WG ? tail_exact(t, kk, p, cin.u, lane, wave, &n, &dbg_p) : -1;
+    int idx = tail_exact(t, kk, p, cin.u, lane, wave, &n, &dbg_p);
     const bool act = lane < kk;
     if (idx < 0) {
         // the chains replayed exactly in reference order: the softmax total (:58)
         int st;
         const auto never = [](double, int) { return false; };
-        const double sum = kk > TAIL_WG ? replay_sum<8>(t, kk, 0.0, never, &st) : replay_sum<1>(t, kk, 0.0, never, &st);
+        const double sum = replay_sum<1>(t, kk, 0.0, never, &st);
         // p_i (:60), and min-p (:62-68): the first candidate i >= 1 with p_i < p_0 * min_p ends the list
         const double e0 = (double) expf_glibc(__fdiv_rn(__fsub_rn(maxl, maxl), p.temperature));
         const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
         if (tid == 0) s_wide_n = kk;
         __syncthreads();
-        if (kk > TAIL_WG)
-            tail_probs<8>(t, kk, sum, thr, p.min_p, tid);
-        else
-            tail_probs<1>(t, kk, sum, thr, p.min_p, tid);
+        if (tid < kk) {
+            const float pi = __double2float_rn(__ddiv_rn(t[tid], sum));
+            if (p.min_p > 0.0f && tid >= 1 && !(pi >= thr)) atomicMin(&s_wide_n, tid);
+            t[tid] = (double) pi;
+        }
         __syncthreads();
         n = s_wide_n;
         dbg_p = act ? (float) t[lane] : 0.0f;
@@ -1957,19 +1921,16 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
         if (p.top_p < 1.0f) {
             const double tp = (double) p.top_p;
             const auto reach = [tp](double acc, int) { return acc >= tp; };
-            total = n > TAIL_WG ? replay_sum<8>(t, n, 0.0, reach, &st) : replay_sum<1>(t, n, 0.0, reach, &st);
+            total = replay_sum<1>(t, n, 0.0, reach, &st);
             n = st >= 0 ? st + 1 : n;
         } else {
-            total = n > TAIL_WG ? replay_sum<8>(t, n, 0.0, never, &st) : replay_sum<1>(t, n, 0.0, never, &st);
+            total = replay_sum<1>(t, n, 0.0, never, &st);
         }
         // draw (:82-88): r = u*(total-0)+0, then r -= p_i until r <= 0 (else the last kept candidate); as a
         // chain of additions of -p_i (exactly the subtractions)
         const double r0 = __dadd_rn(__dmul_rn(cin.u, __dsub_rn(total, 0.0)), 0.0);
         const auto spent = [](double r, int) { return r <= 0.0; };
-        if (n > TAIL_WG)
-            replay_sum<8, true>(t, n, r0, spent, &st);
-        else
-            replay_sum<1, true>(t, n, r0, spent, &st);
+        replay_sum<1, true>(t, n, r0, spent, &st);
         idx = st >= 0 ? st : n - 1;
     }
     if (wave != 0) return;
@@ -1986,14 +1947,318 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
     }
 }
 
-// The wide path's tail: one workgroup per row over the row's part of the sorted key buffer, the terms in the
-// row's part of the (free after the sort) unsorted one.
-__global__ __launch_bounds__(TAIL_WG) void wide_tail_kernel(RowsArgs a, WideArgs w) {
-    const int row = (int) blockIdx.x;
-    const WideKeyFmt fmt{w.id_bits, (1ull << (32 + w.id_bits)) - 1ull, (1u << w.id_bits) - 1u};
-    const CallIn cin = read_call<false>(a, row);
-    sorted_tail(a, row, w.sorted + (int64_t) row * a.V, w.k, reinterpret_cast<double*>(w.keys + (int64_t) row * a.V),
-                cin, fmt);
+// ---- The wide path's tail (src/sampler.cpp:53-88 over every sorted candidate) on many workgroups. Its three
+// double chains (the softmax total, the top-p cumulative sum with the draw's total, the draw's subtractions) are
+// cut into chunks of WT_CHUNK terms, and each chain runs as:
+//   * a map kernel (workgroup = (row, chunk)): the chunk's place in the chain from an approximate prefix (the
+//     earlier chunks' term sums added in any order). The partial results of one chain are monotone (its terms
+//     share a sign), so when the approximate results at the chunk's two ends, widened by a margin, lie in one
+//     binade [2^E, 2^(E+1)) (and, for top-p, below the stop), every exact partial result inside the chunk does
+//     too and none meets the stop: the chunk's terms then compose to one parity map in that binade (as in
+//     replay_sum). Otherwise the chunk is left to be replayed;
+//   * a resolve kernel (one workgroup per row): from the chain's exact start, in order, a run of mapped chunks of
+//     one binade is applied as one composed map and any other chunk is replayed exactly (replay_sum: one block of
+//     two terms per thread), until the chain ends or stops.
+// The margin: with M = |start| + the sum of the chain's |terms|, every rounded partial result of the reference's
+// chain is within j * 2^-53 * M of the exact partial sum after j terms, and the approximate prefix within
+// (chunks + 16) * 2^-53 * M of it (additions of same-signed values in any order); the margin is
+// (n + chunks + 64) * 2^-50 * M, eight times their sum. A resolve kernel checks that the exact result entering a
+// run lies in the run's binade (and replays the chunk if not); a composed result outside the binade would be a
+// broken bound and is reported as a fault.
+// Chunk kernels: WT_WG threads, WT_PT terms each (i = lo + q * WT_WG + tid for the term passes, consecutive runs
+// lo + tid * WT_PT + q where maps are composed in order).
+constexpr int WT_WG = 256, WT_PT = WT_CHUNK / WT_WG;
+constexpr int WT_REC = 512;  // chunk records a resolve kernel holds in LDS at once
+static_assert(WT_CHUNK == 2 * TAIL_WG, "a replayed chunk is one replay_sum block of two terms per thread");
+
+__shared__ double s_wt_red[2][WT_WG / 64];
+__shared__ ParMap s_wt_map[WT_WG / 64];
+__shared__ int s_wt_bad[WT_WG / 64];
+__shared__ WideChunk s_wt_rec[WT_REC];
+
+__device__ __forceinline__ WideKeyFmt wide_fmt(const WideArgs& w) {
+    return WideKeyFmt{w.id_bits, (1ull << (32 + w.id_bits)) - 1ull, (1u << w.id_bits) - 1u};
+}
+// a row's terms: its part of the (free after the sort) unsorted key buffer
+__device__ __forceinline__ double* wide_terms(const RowsArgs& a, const WideArgs& w, int row) {
+    return reinterpret_cast<double*>(w.keys + (int64_t) row * a.V);
+}
+
+// Sum of x over the chunk workgroup, in every thread (slot: which LDS row to use).
+__device__ __forceinline__ double wt_sum(double x, int slot, int lane, int wave) {
+    x = wave_sum_f64(x, lane);
+    if (lane == 0) s_wt_red[slot][wave] = x;
+    __syncthreads();
+    double s = 0.0;
+#pragma unroll
+    for (int o = 0; o < WT_WG / 64; ++o) s += s_wt_red[slot][o];
+    return s;
+}
+
+// Chain PH of a row: 0 the softmax total over the kk candidates from 0 (:58); 1 the cumulative sum over the n_mp
+// kept by min-p from 0, stopping where it reaches top_p when top_p < 1 (:69-81); 2 the draw over the n_top kept,
+// r0 - p_0 - p_1 - ..., stopping at r <= 0 (:82-88).
+template <int PH>
+struct WtChain {
+    int n;
+    double a0;
+    int mode;    // 0: no stop, 1: stop at acc >= thr, 2: stop at acc <= 0
+    double thr;
+    static constexpr bool NEG = PH == 2;
+    __device__ WtChain(const RowsArgs& a, const WideRow& rs) {
+        n = PH == 0 ? rs.kk : PH == 1 ? rs.n_mp : rs.n_top;
+        a0 = PH == 2 ? rs.r0 : 0.0;
+        mode = PH == 2 ? 2 : (PH == 1 && a.p.top_p < 1.0f) ? 1 : 0;
+        thr = (double) a.p.top_p;
+    }
+};
+
+// e_i (:55-58) of the row's first w.k sorted keys, their chunk sums, and the candidate count kk (the first NaN key
+// ends the candidates: written by the one thread whose key is the first NaN, or holds the last key if none is).
+__global__ __launch_bounds__(WT_WG) void wt_terms_kernel(RowsArgs a, WideArgs w) {
+    const int row = (int) blockIdx.x / w.chunks, c = (int) blockIdx.x - row * w.chunks;
+    const int tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const WideKeyFmt fmt = wide_fmt(w);
+    const uint64_t* K = w.sorted + (int64_t) row * a.V;
+    double* t = wide_terms(a, w, row);
+    const int k = w.k, lo = c * WT_CHUNK;
+    const uint64_t etab = kExp2Tab[lane & 31];
+    uint32_t o[WT_PT];
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) o[q] = fmt.img(K[min(lo + q * WT_WG + tid, k - 1)]);
+    const float maxl = unord_f32(fmt.img(K[0]));
+    double s = 0.0;
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) {
+        const int i = lo + q * WT_WG + tid;
+        const float e = expf_glibc_tab(__fdiv_rn(__fsub_rn(unord_f32(o[q]), maxl), a.p.temperature), etab);
+        if (i < k) {
+            const double ed = o[q] != 0u ? (double) e : 0.0;
+            t[i] = ed;
+            s += ed;
+            if (o[q] == 0u ? (i == 0 || fmt.img(K[i - 1]) != 0u) : i == k - 1)
+                w.rowst[row].kk = o[q] == 0u ? i : k;
+        }
+    }
+    s = wt_sum(s, 0, lane, wave);
+    if (tid == 0) w.part[(int64_t) row * w.chunks + c] = s;
+}
+
+// p_i = (float) (e_i / sum) (:60) in place, min-p (:62-68: n_mp lowered to the first i >= 1 with p_i < p_0 *
+// min_p; the resolve of chain 0 set it to kk), and the chunk sums of the p_i.
+__global__ __launch_bounds__(WT_WG) void wt_probs_kernel(RowsArgs a, WideArgs w) {
+    const int row = (int) blockIdx.x / w.chunks, c = (int) blockIdx.x - row * w.chunks;
+    const int tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const WideKeyFmt fmt = wide_fmt(w);
+    const int kk = w.rowst[row].kk, lo = c * WT_CHUNK;
+    if (lo >= kk) return;  // (uniform)
+    const double sum = w.rowst[row].sum;
+    double* t = wide_terms(a, w, row);
+    double e[WT_PT];
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) e[q] = t[min(lo + q * WT_WG + tid, kk - 1)];
+    const float maxl = unord_f32(fmt.img(w.sorted[(int64_t) row * a.V]));
+    const double e0 = (double) expf_glibc(__fdiv_rn(__fsub_rn(maxl, maxl), a.p.temperature));
+    const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), a.p.min_p);
+    double s = 0.0;
+    int fail = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) {
+        const int i = lo + q * WT_WG + tid;
+        if (i < kk) {
+            const float pi = __double2float_rn(__ddiv_rn(e[q], sum));
+            if (a.p.min_p > 0.0f && i >= 1 && !(pi >= thr)) fail = min(fail, i);
+            t[i] = (double) pi;
+            s += (double) pi;
+        }
+    }
+    s = wt_sum(s, 0, lane, wave);
+    const uint64_t fb = ballot(fail != 0x7fffffff);
+    if (fb) {
+        int m = fail;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) m = min(m, __shfl_xor(m, d, 64));
+        if (lane == 0) atomicMin(&w.rowst[row].n_mp, m);
+    }
+    if (tid == 0) w.part[(int64_t) row * w.chunks + c] = s;
+}
+
+// The chunk's record for chain PH (see above).
+template <int PH>
+__global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) {
+    const int row = (int) blockIdx.x / w.chunks, c = (int) blockIdx.x - row * w.chunks;
+    const int tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const WtChain<PH> ch(a, w.rowst[row]);
+    const int n = ch.n, lo = c * WT_CHUNK;
+    if (lo >= n) return;  // (uniform)
+    const int nc = (n + WT_CHUNK - 1) / WT_CHUNK;
+    const double* t = wide_terms(a, w, row);
+    const int j0 = lo + tid * WT_PT;
+    double tv[WT_PT];
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) tv[q] = t[min(j0 + q, n - 1)];
+    // the earlier chunks' sums (pre) and every chunk's of the chain (all: for M), and this chunk's own
+    double pre = 0.0, all = 0.0, own = 0.0;
+    for (int j = tid; j < nc; j += WT_WG) {
+        const double v = w.part[(int64_t) row * w.chunks + j];
+        pre += j < c ? v : 0.0;
+        all += v;
+    }
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) own += j0 + q < n ? tv[q] : 0.0;
+    pre = wt_sum(pre, 0, lane, wave);
+    all = wt_sum(all, 1, lane, wave);
+    __syncthreads();  // (the first sum's LDS row is reused)
+    own = wt_sum(own, 0, lane, wave);
+    const double ps = ch.NEG ? ch.a0 - pre : ch.a0 + pre;
+    const double pe = ch.NEG ? ps - own : ps + own;
+    const double margin = (fabs(ch.a0) + all) * ((double) n + (double) nc + 64.0) * 0x1p-50;
+    const double lo_b = fmin(ps, pe) - margin, hi_b = fmax(ps, pe) + margin;
+    int E = 0;
+    bool ok = lo_b >= 0x1p-1000 && hi_b <= 0x1p1000;  // (false for NaN: the chunk is replayed)
+    if (ok) {
+        (void) frexp(lo_b, &E);
+        E -= 1;  // lo_b in [2^E, 2^(E+1))
+        ok = hi_b < ldexp(1.0, E + 1) && !(ch.mode == 1 && !(hi_b < ch.thr));
+    }
+    ParMap m = par_identity();
+    bool bad = false;
+    if (ok) {  // (uniform)
+#pragma unroll
+        for (int q = 0; q < WT_PT; ++q) {
+            double f;
+            bool cr;
+            const ParMap tm = term_map(ch.NEG ? -tv[q] : tv[q], E, &f, &cr);
+            if (j0 + q < n) {
+                bad |= cr;
+                m = par_compose(m, tm);
+            }
+        }
+        m = wave_scan_map<false>(m);
+        if (lane == 63) s_wt_map[wave] = m;
+        const uint64_t bb = ballot(bad);
+        if (lane == 0) s_wt_bad[wave] = bb != 0ull;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        WideChunk r{0.0, 0.0, 2u, E, 0, 0};
+        if (ok) {
+            ParMap x = s_wt_map[0];
+            bool anybad = s_wt_bad[0] != 0;
+#pragma unroll
+            for (int o = 1; o < WT_WG / 64; ++o) {
+                x = par_compose(x, s_wt_map[o]);
+                anybad |= s_wt_bad[o] != 0;
+            }
+            if (!anybad) r = WideChunk{x.d0, x.d1, x.p, E, 1, 0};
+        }
+        w.chunk[(int64_t) row * w.chunks + c] = r;
+    }
+}
+
+// Chain PH of one row from its exact start, with the whole workgroup (uniform control flow): returns the last
+// partial result and the stop index (-1: none).
+template <int PH, typename F>
+__device__ double wt_resolve(const RowsArgs& a, const WideArgs& w, int row, const WtChain<PH>& ch, F stop,
+                             int* stopped) {
+    const int tid = (int) threadIdx.x, lane = tid & 63;
+    const int n = ch.n, nc = (n + WT_CHUNK - 1) / WT_CHUNK;
+    const double* t = wide_terms(a, w, row);
+    const WideChunk* rec = w.chunk + (int64_t) row * w.chunks;
+    double acc = ch.a0;
+    int st = -1, c = 0, wb = -WT_REC;  // wb: the first chunk of the records held in LDS
+    while (c < nc) {
+        if (c >= wb + WT_REC || c + 64 > wb + WT_REC) {  // (re)load the window of records from c on
+            __syncthreads();
+            wb = c;
+            for (int j = tid; j < WT_REC && wb + j < nc; j += TAIL_WG) s_wt_rec[j] = rec[wb + j];
+            __syncthreads();
+        }
+        const WideChunk r0 = s_wt_rec[c - wb];
+        bool in = false;
+        if (r0.mapped) {
+            int E;
+            (void) frexp(acc, &E);
+            in = acc >= 0x1p-1000 && acc <= 0x1p1000 && E - 1 == r0.E;
+        }
+        if (in) {  // (uniform) a run of mapped chunks of r0's binade, at most 64
+            const int cj = c + lane;
+            const WideChunk r = cj < nc ? s_wt_rec[cj - wb] : WideChunk{0.0, 0.0, 2u, 0, 0, 0};
+            const uint64_t run = ballot(cj < nc && r.mapped && r.E == r0.E);
+            const int len = ~run ? (int) __builtin_ctzll(~run) : 64;  // >= 1 (lane 0 is in the run)
+            ParMap x = lane < len ? ParMap{r.d0, r.d1, r.p} : par_identity();
+            x = wave_scan_map<false>(x);
+            const ParMap tot = rdlane_map(x, 63);
+            double A = ldexp(acc, 52 - r0.E);
+            A += dparity(A) ? tot.d1 : tot.d0;
+            if (!(A >= 0x1p52 && A < 0x1p53) && tid == 0) report_fault(a, FAULT_WIDE_MAP);
+            acc = ldexp(A, r0.E - 52);
+            c += len;
+        } else {
+            const int lo = c * WT_CHUNK, len = min(WT_CHUNK, n - lo);
+            int s2;
+            acc = replay_sum<2, WtChain<PH>::NEG>(t + lo, len, acc, stop, &s2);
+            if (s2 >= 0) {
+                st = lo + s2;
+                break;
+            }
+            ++c;
+        }
+    }
+    *stopped = st;
+    return acc;
+}
+
+// Resolves chain PH of each row (one workgroup per row) and hands its results to the next kernels; the last
+// publishes the row's token.
+template <int PH>
+__global__ __launch_bounds__(TAIL_WG) void wt_resolve_kernel(RowsArgs a, WideArgs w) {
+    const int row = (int) blockIdx.x, tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    WideRow* rs = w.rowst + row;
+    const WtChain<PH> ch(a, *rs);
+    int st = -1;
+    double acc = ch.a0;
+    if (ch.n > 0) {
+        if (ch.mode == 1) {
+            const double thr = ch.thr;
+            acc = wt_resolve<PH>(a, w, row, ch, [thr](double x, int) { return x >= thr; }, &st);
+        } else if (ch.mode == 2) {
+            acc = wt_resolve<PH>(a, w, row, ch, [](double x, int) { return x <= 0.0; }, &st);
+        } else {
+            acc = wt_resolve<PH>(a, w, row, ch, [](double, int) { return false; }, &st);
+        }
+    }
+    if (tid != 0 && PH != 2) return;
+    if (PH == 0) {
+        rs->sum = acc;
+        rs->n_mp = ch.n;  // (min-p lowers it)
+    } else if (PH == 1) {
+        // top-p (:70-79) keeps up to the stop; the draw's total (:80-81) is the chain's result there
+        const int n_top = st >= 0 ? st + 1 : ch.n;
+        const double u = read_call<false>(a, row).u;
+        rs->n_top = n_top;
+        rs->total = acc;
+        rs->r0 = __dadd_rn(__dmul_rn(u, __dsub_rn(acc, 0.0)), 0.0);
+    } else {
+        if (wave != 0) return;
+        const WideKeyFmt fmt = wide_fmt(w);
+        const uint64_t* K = w.sorted + (int64_t) row * a.V;
+        const int kk = rs->kk, n_top = ch.n;
+        const CallIn cin = read_call<false>(a, row);
+        const int idx = st >= 0 ? st : n_top - 1;
+        const int tok = kk > 0 ? fmt.id(K[idx]) : 0;  // no number in the row: the fast path's empty list
+        const bool act = lane < kk;
+        const uint64_t kl = act ? K[lane] : 0ull;
+        if (a.dbg_keys) a.dbg_keys[row * KCAP + lane] = act ? ((uint64_t) fmt.img(kl) << 32) | (uint64_t) ~(uint32_t) fmt.id(kl) : 0ull;
+        if (a.dbg_probs) a.dbg_probs[row * KCAP + lane] = act ? (float) wide_terms(a, w, row)[lane] : 0.0f;
+        if (lane == 0) {
+            if (a.dbg_meta) {
+                a.dbg_meta[row * 2] = kk;
+                a.dbg_meta[row * 2 + 1] = kk > 0 ? n_top : 0;
+            }
+            publish(a, row, tok, cin.seq, cin.draft);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -2016,6 +2281,7 @@ constexpr int MID_NW = 16, MID_WG = MID_NW * 64, MID_EPT = 32, MID_RK = MID_ROWC
 constexpr int MID_SORT = 4096;  // keys the row's sort holds
 static_assert(MID_WG * MID_EPT == MID_SEG, "segment length");
 static_assert(MID_WG == TAIL_WG, "the row's tail runs on the mid workgroup");
+static_assert(MID_KMAX <= TAIL_WG, "sorted_tail holds one candidate per thread");
 static_assert(MID_KMAX <= MID_NW * 64, "a wave's bound index is at most 64");
 static_assert(MID_SORT == 4 * MID_WG && MID_SORT >= MID_KMAX, "the sort's layout");
 
@@ -2394,7 +2660,7 @@ int wide_id_bits(int V) {
 }
 
 hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipStream_t s) {
-    if (w.k <= KCAP || w.k > a.V) return hipErrorInvalidValue;
+    if (w.k <= KCAP || w.k > a.V || w.chunks != (w.k + WT_CHUNK - 1) / WT_CHUNK) return hipErrorInvalidValue;
     const int segs = (a.V + WIDE_SEG - 1) / WIDE_SEG;
     const dim3 grid((unsigned) (a.n_rows * segs));
     if (penalize)
@@ -2411,11 +2677,20 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
     // alone leaves equal values in ascending id order, as the id field would: its passes are skipped.
     e = sort_keys_desc(w.keys, w.sorted, n, w.id_bits, 32 + w.id_bits + rb, w.counts, &sorted, s);
     if (e != hipSuccess) return e;
-    // the tail reads the sorted buffer and keeps its terms in the other one
+    // the tail reads the sorted buffer and keeps its terms in the other one: the three chains, each mapped per
+    // chunk and resolved per row
     WideArgs t = w;
     t.sorted = sorted;
     t.keys = sorted == w.keys ? w.sorted : w.keys;
-    hipLaunchKernelGGL(wide_tail_kernel, dim3((unsigned) a.n_rows), dim3(TAIL_WG), 0, s, a, t);
+    const dim3 gc((unsigned) (a.n_rows * w.chunks)), gr((unsigned) a.n_rows);
+    hipLaunchKernelGGL(wt_terms_kernel, gc, dim3(WT_WG), 0, s, a, t);
+    hipLaunchKernelGGL(wt_maps_kernel<0>, gc, dim3(WT_WG), 0, s, a, t);
+    hipLaunchKernelGGL(wt_resolve_kernel<0>, gr, dim3(TAIL_WG), 0, s, a, t);
+    hipLaunchKernelGGL(wt_probs_kernel, gc, dim3(WT_WG), 0, s, a, t);
+    hipLaunchKernelGGL(wt_maps_kernel<1>, gc, dim3(WT_WG), 0, s, a, t);
+    hipLaunchKernelGGL(wt_resolve_kernel<1>, gr, dim3(TAIL_WG), 0, s, a, t);
+    hipLaunchKernelGGL(wt_maps_kernel<2>, gc, dim3(WT_WG), 0, s, a, t);
+    hipLaunchKernelGGL(wt_resolve_kernel<2>, gr, dim3(TAIL_WG), 0, s, a, t);
     return hipGetLastError();
 }
 

@@ -117,6 +117,48 @@ def test_wide_batch(torch_cuda, K, oracle_lib, case):
     S.close()
 
 
+# The wide tail's chunked chains: rows whose sums cross many binades over many chunks (flat logits), top-p at 1
+# (no stop), min-p cutting inside a chunk, a k that ends inside a chunk, bf16-valued rows (runs of equal terms),
+# low and high temperatures, and uniforms 0 and 0.9999999 (the draw stopping at once / running to the end).
+# V, rows, temperature, top_k, top_p, min_p, kind
+CHUNK_CASES = [
+    (248320, 3, 1.0, 0, 0.95, 0.0, "flat"),
+    (248320, 3, 0.35, 0, 1.0, 0.0, "flat"),
+    (100003, 3, 1.7, 0, 0.9, 1e-5, "flat"),
+    (248320, 3, 1.0, 5000, 0.99, 0.0, "heads"),
+    (248320, 3, 1.0, 0, 0.95, 0.0, "bf16"),
+    (65536, 3, 3.0, 0, 0.999, 0.0, "flat"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CHUNK_CASES)))
+def test_wide_chunked_chains(torch_cuda, K, oracle_lib, case):
+    torch = torch_cuda
+    O = oracle_lib
+    V, rows, T, k, tp, mp, kind = CHUNK_CASES[case]
+    rng = np.random.default_rng(1700 + case)
+    if kind == "heads":
+        x = head_rows(rng, rows, V)
+    else:
+        x = (rng.standard_normal((rows, V)) * (2.0 if V == 100003 else 1.0)).astype(np.float32)
+        if kind == "bf16":
+            x = (x.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    p = W.Params(temperature=T, top_k=k, top_p=tp, min_p=mp)
+    u = np.array([0.0, 0.9999999, rng.random()])
+    S = K.Sampler(p, n_vocab=V, max_rows=rows)
+    assert S.path == "wide", (case, S.path)
+    out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    say("wide chunked chains", case, "V", V, "k", k, kind)
+    S.sample_batch(dev(torch, x), dev(torch, u), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        t = check_row(S, O, x[r], p, u[r], None, r, f"chunks{case}")
+        assert got[r] == t, (case, r, got[r], t)
+    S.check()
+    S.close()
+
+
 def test_wide_ties_and_infinities(torch_cuda, K, oracle_lib):
     """Every logit equal (candidate order is id order), and rows with -inf logits, under no top-k limit."""
     torch = torch_cuda
