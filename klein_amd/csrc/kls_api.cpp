@@ -517,7 +517,7 @@ int kls_destroy(kls_handle h) {
     void* dev[] = {h->d_hist_ids, h->d_hist_w, h->d_hist_boff, h->d_seg_cand,
                    h->d_row_ticket, h->d_row_thr, h->d_tokens, h->d_accepted,
                    h->d_step, h->d_dbg_keys, h->d_dbg_probs, h->d_dbg_meta,
-                   h->d_rows_buf, h->w.keys, h->w.sorted, h->w.counts, h->w.part, h->w.chunk, h->w.rowst,
+                   h->d_rows_buf, h->w.keys, h->w.sorted, h->w.counts, h->w.part, h->w.seg, h->w.nseg, h->w.rowst,
                    h->m.buf, h->m.fill};
     for (void* p : dev)
         if (p) (void) hipFree(p);
@@ -608,7 +608,8 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
         ALLOC(h->w.counts, sizeof(uint32_t) * 256 * sort_tiles(R * (size_t) n_vocab));
         h->w.chunks = (k + WT_CHUNK - 1) / WT_CHUNK;
         ALLOC(h->w.part, sizeof(double) * R * h->w.chunks);
-        ALLOC(h->w.chunk, sizeof(WideChunk) * R * h->w.chunks);
+        ALLOC(h->w.seg, sizeof(WideSeg) * R * h->w.chunks * WT_SEGS);
+        ALLOC(h->w.nseg, sizeof(int32_t) * R * h->w.chunks);
         ALLOC(h->w.rowst, sizeof(WideRow) * R);
     }
 #undef ALLOC

@@ -48,7 +48,7 @@ struct ResultBlock {
 constexpr uint32_t FAULT_COUNT_WAIT = 1;   // the history count table was not announced complete in time
 constexpr uint32_t FAULT_BOUND_WAIT = 2;   // the early bound of a 16-wave segment was not published in time
 constexpr uint32_t FAULT_NARROW = 3;       // a mid top-k threshold bisection did not end (not reachable)
-constexpr uint32_t FAULT_WIDE_MAP = 4;     // a chunk map of the wide tail left its binade (not reachable)
+constexpr uint32_t FAULT_WIDE_MAP = 4;     // a segment map of the wide tail left its binade (not reachable)
 
 struct SamplingParams {
     float temperature;
@@ -126,15 +126,20 @@ constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 20;
 // with row field = n_rows - 1 - row, so one descending device-wide sort of all rows' keys leaves each row's keys
 // contiguous, value-descending and, on equal values, id-ascending (the fast path's order). NaN maps to the
 // value image 0, after every number. The sorted keys then go through the O(k) tail in reference order.
-// The wide path's tail cuts each of its double chains into chunks of WT_CHUNK terms (kls_kernels.hip):
-constexpr int WT_CHUNK = 2048;
-// a chunk's place in the chain being resolved: its terms composed to one parity map in the binade 2^E when
-// `mapped` (else it is replayed term by term)
-struct WideChunk {
-    double d0, d1;  // increments in units of 2^(E-52) from an incoming even / odd partial result
-    uint32_t p;     // parity after: bit 0 from even, bit 1 from odd
+// The wide path's tail cuts each of its double chains into chunks of WT_CHUNK terms (kls_kernels.hip), and each
+// chunk into at most WT_SEGS segments, recorded in order:
+constexpr int WT_CHUNK = 2048, WT_SEGS = 32;
+enum : int32_t {
+    WS_MAP = 1,     // terms [start, end) composed to one parity map in the binade 2^E
+    WS_TERM = 2,    // one term (d0, signed as the chain adds it) added on its own
+    WS_REPLAY = 3,  // terms [start, end) replayed one by one (a chunk of more than WT_SEGS segments)
+};
+struct WideSeg {
+    double d0, d1;  // WS_MAP: increments in units of 2^(E-52) from an incoming even / odd partial result
+    uint32_t p;     // WS_MAP: parity after, bit 0 from even, bit 1 from odd
     int32_t E;
-    int32_t mapped;
+    int32_t kind;
+    int32_t start, end;
     int32_t pad;
 };
 // a row's state between the tail's kernels
@@ -156,7 +161,8 @@ struct WideArgs {
     int32_t id_bits;      // ids are below 1 << id_bits
     int32_t chunks;       // chunks per row: ceil(k / WT_CHUNK)
     double* part;         // [max_rows * chunks] term sums of the chunks
-    WideChunk* chunk;     // [max_rows * chunks]
+    WideSeg* seg;         // [max_rows * chunks * WT_SEGS] the chunks' segments of the chain being resolved
+    int32_t* nseg;        // [max_rows * chunks] segments per chunk
     WideRow* rowst;       // [max_rows]
 };
 

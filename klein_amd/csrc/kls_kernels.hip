@@ -1950,31 +1950,57 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
 // ---- The wide path's tail (src/sampler.cpp:53-88 over every sorted candidate) on many workgroups. Its three
 // double chains (the softmax total, the top-p cumulative sum with the draw's total, the draw's subtractions) are
 // cut into chunks of WT_CHUNK terms, and each chain runs as:
-//   * a map kernel (workgroup = (row, chunk)): the chunk's place in the chain from an approximate prefix (the
-//     earlier chunks' term sums added in any order). The partial results of one chain are monotone (its terms
-//     share a sign), so when the approximate results at the chunk's two ends, widened by a margin, lie in one
-//     binade [2^E, 2^(E+1)) (and, for top-p, below the stop), every exact partial result inside the chunk does
-//     too and none meets the stop: the chunk's terms then compose to one parity map in that binade (as in
-//     replay_sum). Otherwise the chunk is left to be replayed;
-//   * a resolve kernel (one workgroup per row): from the chain's exact start, in order, a run of mapped chunks of
-//     one binade is applied as one composed map and any other chunk is replayed exactly (replay_sum: one block of
-//     two terms per thread), until the chain ends or stops.
+//   * a map kernel (workgroup = (row, chunk)): every term's place in the chain from an approximate prefix (the
+//     earlier chunks' term sums and a scan of the chunk's own, added in any order). A term whose approximate
+//     partial results before and after it, widened by a margin, lie in one binade [2^E, 2^(E+1)) (and, for
+//     top-p, below the stop) has exact partial results there too and does not meet the stop: its map in that
+//     binade (term_map) is valid. The chunk is cut into segments, in order: maximal runs of such terms in one
+//     binade, composed to one map (a segmented scan), and every other term on its own (binade crossings, the
+//     stop, the start from 0). Terms whose approximate partial result before them is past the stop by the
+//     margin are left out (the exact chain has stopped before them). A chunk of more than WT_SEGS segments is
+//     recorded as one segment to replay;
+//   * a resolve kernel (one workgroup per row): from the chain's exact start, the segments in order: runs of
+//     mapped segments of one binade are applied as one composed map (64 at a time), a single term is added, a
+//     segment to replay goes through replay_sum; a mapped segment whose composed results reach the stop, or that
+//     the exact partial result enters outside its binade, is replayed term by term.
 // The margin: with M = |start| + the sum of the chain's |terms|, every rounded partial result of the reference's
 // chain is within j * 2^-53 * M of the exact partial sum after j terms, and the approximate prefix within
-// (chunks + 16) * 2^-53 * M of it (additions of same-signed values in any order); the margin is
-// (n + chunks + 64) * 2^-50 * M, eight times their sum. A resolve kernel checks that the exact result entering a
-// run lies in the run's binade (and replays the chunk if not); a composed result outside the binade would be a
-// broken bound and is reported as a fault.
-// Chunk kernels: WT_WG threads, WT_PT terms each (i = lo + q * WT_WG + tid for the term passes, consecutive runs
-// lo + tid * WT_PT + q where maps are composed in order).
+// (chunks + 2 * WT_CHUNK + 16) * 2^-53 * M of it (additions of same-signed values in any order); the margin is
+// (n + chunks + 2 * WT_CHUNK + 64) * 2^-50 * M, more than eight times their sum. A composed result outside its
+// binade would be a broken bound and is reported as a fault.
+// Chunk kernels: WT_WG threads, WT_PT terms each (i = lo + q * WT_WG + tid for the term passes; consecutive
+// runs lo + tid * WT_PT + q where maps are composed in order).
 constexpr int WT_WG = 256, WT_PT = WT_CHUNK / WT_WG;
-constexpr int WT_REC = 512;  // chunk records a resolve kernel holds in LDS at once
-static_assert(WT_CHUNK == 2 * TAIL_WG, "a replayed chunk is one replay_sum block of two terms per thread");
+constexpr int WT_WIN = 48;  // chunks whose segments a resolve kernel holds in LDS at once
+static_assert(WT_WIN <= 64, "one wave scans the window's segment counts");
+static_assert(WT_CHUNK == 2 * TAIL_WG, "a replayed segment is at most one replay_sum block of two terms per thread");
+// segment codes of a term on its own / past n or past the stop
+constexpr int CODE_HARD = -0x7fffffff, CODE_NONE = -0x7ffffffe;
 
 __shared__ double s_wt_red[2][WT_WG / 64];
 __shared__ ParMap s_wt_map[WT_WG / 64];
-__shared__ int s_wt_bad[WT_WG / 64];
-__shared__ WideChunk s_wt_rec[WT_REC];
+__shared__ int s_wt_code[WT_WG / 64], s_wt_head[WT_WG / 64], s_wt_hcnt[WT_WG / 64];
+__shared__ WideSeg s_wt_seg[WT_SEGS];
+__shared__ int s_wt_start[WT_SEGS];
+__shared__ WideSeg s_wt_flat[WT_WIN * WT_SEGS];
+__shared__ int s_wt_off[WT_WIN + 1];
+
+// Composition for a segmented scan: bit 2 of p marks a map that starts a segment (nothing before it applies).
+__device__ __forceinline__ ParMap seg_compose(const ParMap& e, const ParMap& l) {
+    if (l.p & 4u) return l;
+    ParMap c = par_compose(e, l);
+    c.p |= e.p & 4u;
+    return c;
+}
+__device__ __forceinline__ ParMap wave_seg_scan(ParMap x) {
+    x = seg_compose(dpp_map<0x111, 0xf>(x), x);
+    x = seg_compose(dpp_map<0x112, 0xf>(x), x);
+    x = seg_compose(dpp_map<0x114, 0xf>(x), x);
+    x = seg_compose(dpp_map<0x118, 0xf>(x), x);
+    x = seg_compose(dpp_map<0x142, 0xa>(x), x);
+    x = seg_compose(dpp_map<0x143, 0xc>(x), x);
+    return x;
+}
 
 __device__ __forceinline__ WideKeyFmt wide_fmt(const WideArgs& w) {
     return WideKeyFmt{w.id_bits, (1ull << (32 + w.id_bits)) - 1ull, (1u << w.id_bits) - 1u};
@@ -2083,7 +2109,7 @@ __global__ __launch_bounds__(WT_WG) void wt_probs_kernel(RowsArgs a, WideArgs w)
     if (tid == 0) w.part[(int64_t) row * w.chunks + c] = s;
 }
 
-// The chunk's record for chain PH (see above).
+// The segments of a chunk of chain PH (see above).
 template <int PH>
 __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) {
     const int row = (int) blockIdx.x / w.chunks, c = (int) blockIdx.x - row * w.chunks;
@@ -2091,13 +2117,16 @@ __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) 
     const WtChain<PH> ch(a, w.rowst[row]);
     const int n = ch.n, lo = c * WT_CHUNK;
     if (lo >= n) return;  // (uniform)
-    const int nc = (n + WT_CHUNK - 1) / WT_CHUNK;
+    const int nc = (n + WT_CHUNK - 1) / WT_CHUNK, last = min(n, lo + WT_CHUNK) - 1;
     const double* t = wide_terms(a, w, row);
     const int j0 = lo + tid * WT_PT;
-    double tv[WT_PT];
+    double sv[WT_PT];  // the terms as the chain adds them (0 past n)
 #pragma unroll
-    for (int q = 0; q < WT_PT; ++q) tv[q] = t[min(j0 + q, n - 1)];
-    // the earlier chunks' sums (pre) and every chunk's of the chain (all: for M), and this chunk's own
+    for (int q = 0; q < WT_PT; ++q) {
+        const double x = t[min(j0 + q, n - 1)];
+        sv[q] = j0 + q < n ? (ch.NEG ? -x : x) : 0.0;
+    }
+    // approximate partial results: the earlier chunks' sums, then an exclusive scan of the threads' sums
     double pre = 0.0, all = 0.0, own = 0.0;
     for (int j = tid; j < nc; j += WT_WG) {
         const double v = w.part[(int64_t) row * w.chunks + j];
@@ -2105,55 +2134,132 @@ __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) 
         all += v;
     }
 #pragma unroll
-    for (int q = 0; q < WT_PT; ++q) own += j0 + q < n ? tv[q] : 0.0;
+    for (int q = 0; q < WT_PT; ++q) own += sv[q];
     pre = wt_sum(pre, 0, lane, wave);
     all = wt_sum(all, 1, lane, wave);
-    __syncthreads();  // (the first sum's LDS row is reused)
-    own = wt_sum(own, 0, lane, wave);
-    const double ps = ch.NEG ? ch.a0 - pre : ch.a0 + pre;
-    const double pe = ch.NEG ? ps - own : ps + own;
-    const double margin = (fabs(ch.a0) + all) * ((double) n + (double) nc + 64.0) * 0x1p-50;
-    const double lo_b = fmin(ps, pe) - margin, hi_b = fmax(ps, pe) + margin;
-    int E = 0;
-    bool ok = lo_b >= 0x1p-1000 && hi_b <= 0x1p1000;  // (false for NaN: the chunk is replayed)
-    if (ok) {
-        (void) frexp(lo_b, &E);
-        E -= 1;  // lo_b in [2^E, 2^(E+1))
-        ok = hi_b < ldexp(1.0, E + 1) && !(ch.mode == 1 && !(hi_b < ch.thr));
+    const double incl = wave_scan_f64(own);
+    __syncthreads();  // (the sums' LDS rows are reused)
+    if (lane == 63) s_wt_red[0][wave] = incl;
+    __syncthreads();
+    double run = (ch.NEG ? ch.a0 - pre : ch.a0 + pre) + (incl - own);
+#pragma unroll
+    for (int o = 0; o < WT_WG / 64; ++o) run += o < wave ? s_wt_red[0][o] : 0.0;
+    const double margin = (fabs(ch.a0) + all) * ((double) n + (double) nc + 2.0 * WT_CHUNK + 64.0) * 0x1p-50;
+    // each term's binade (code: E) when its map is valid, else CODE_HARD
+    ParMap m[WT_PT];
+    int code[WT_PT];
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) {
+        const double before = run, after = run + sv[q];
+        run = after;
+        const double lb = fmin(before, after) - margin, hb = fmax(before, after) + margin;
+        int E = 0;
+        bool easy = lb >= 0x1p-1000 && hb <= 0x1p1000;  // (false for NaN)
+        if (easy) {
+            (void) frexp(lb, &E);
+            E -= 1;  // lb in [2^E, 2^(E+1))
+            easy = hb < ldexp(1.0, E + 1) && !(ch.mode == 1 && !(hb < ch.thr));
+        }
+        double f;
+        bool cr;
+        m[q] = term_map(sv[q], E, &f, &cr);
+        const bool past = (ch.mode == 1 && before - margin >= ch.thr) || (ch.mode == 2 && before + margin <= 0.0);
+        code[q] = (j0 + q >= n || past) ? CODE_NONE : (easy && !cr) ? E : CODE_HARD;
     }
-    ParMap m = par_identity();
-    bool bad = false;
-    if (ok) {  // (uniform)
+    // segment heads: the chunk's first term, a term on its own, and a term after one or in another binade
+    int prev = __shfl_up(code[WT_PT - 1], 1, 64);
+    if (lane == 63) s_wt_code[wave] = code[WT_PT - 1];
+    bool head[WT_PT];
+    int hc = 0;
+    __syncthreads();
+    if (lane == 0) prev = wave > 0 ? s_wt_code[wave - 1] : CODE_NONE;
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) {
+        const int pc = q == 0 ? prev : code[q - 1];
+        head[q] = code[q] != CODE_NONE && ((tid == 0 && q == 0) || code[q] == CODE_HARD || pc != code[q]);
+        hc += head[q] ? 1 : 0;
+    }
+    // whether the next term starts a segment or is left out (for a thread's last term: the next thread's first)
+    const int brk0 = (head[0] || code[0] == CODE_NONE) ? 1 : 0;
+    int nh = __shfl_down(brk0, 1, 64);
+    if (lane == 0) s_wt_head[wave] = brk0;
+    // segment ordinals: an inclusive scan of the heads
+    int hi = hc;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(hi, d, 64);
+        hi += lane >= d ? y : 0;
+    }
+    if (lane == 63) s_wt_hcnt[wave] = hi;
+    // segmented scan of the maps: each thread's summary, then the wave's and the waves'
+    ParMap T = par_identity();
+#pragma unroll
+    for (int q = 0; q < WT_PT; ++q) {
+        ParMap x = code[q] > CODE_NONE ? m[q] : par_identity();
+        if (head[q]) x.p |= 4u;
+        T = seg_compose(T, x);
+    }
+    const ParMap ti = wave_seg_scan(T);
+    const ParMap te = dpp_map<0x138, 0xf>(ti);  // wave_shr:1: the threads before this one (lane 0: identity)
+    if (lane == 63) s_wt_map[wave] = ti;
+    __syncthreads();
+    if (lane == 63) nh = wave + 1 < WT_WG / 64 ? s_wt_head[wave + 1] : 1;
+    int hbase = hi - hc, htot = 0;
+    ParMap win = par_identity();
+#pragma unroll
+    for (int o = 0; o < WT_WG / 64; ++o) {
+        const int v = s_wt_hcnt[o];
+        hbase += o < wave ? v : 0;
+        htot += v;
+        if (o < wave) win = seg_compose(win, s_wt_map[o]);
+    }
+    const bool over = htot > WT_SEGS;  // (uniform)
+    if (!over) {
+        // each segment's record at its last term (its start at its head)
+        ParMap R = seg_compose(win, te);
+        int ord = hbase - 1;
 #pragma unroll
         for (int q = 0; q < WT_PT; ++q) {
-            double f;
-            bool cr;
-            const ParMap tm = term_map(ch.NEG ? -tv[q] : tv[q], E, &f, &cr);
-            if (j0 + q < n) {
-                bad |= cr;
-                m = par_compose(m, tm);
+            const int j = j0 + q;
+            if (code[q] != CODE_NONE) {
+                if (head[q]) {
+                    ++ord;
+                    R = par_identity();
+                    s_wt_start[ord] = j;
+                }
+                if (code[q] != CODE_HARD) R = par_compose(R, m[q]);
+                const bool ends = j == last || (q + 1 < WT_PT ? head[q + 1] || code[q + 1] == CODE_NONE : nh != 0);
+                if (ends) {
+                    WideSeg r;
+                    r.kind = code[q] == CODE_HARD ? WS_TERM : WS_MAP;
+                    r.d0 = code[q] == CODE_HARD ? sv[q] : R.d0;
+                    r.d1 = R.d1;
+                    r.p = R.p & 3u;
+                    r.E = code[q] == CODE_HARD ? 0 : code[q];
+                    r.start = 0;
+                    r.end = j + 1;
+                    r.pad = 0;
+                    s_wt_seg[ord] = r;
+                }
             }
         }
-        m = wave_scan_map<false>(m);
-        if (lane == 63) s_wt_map[wave] = m;
-        const uint64_t bb = ballot(bad);
-        if (lane == 0) s_wt_bad[wave] = bb != 0ull;
-        __syncthreads();
     }
-    if (tid == 0) {
-        WideChunk r{0.0, 0.0, 2u, E, 0, 0};
-        if (ok) {
-            ParMap x = s_wt_map[0];
-            bool anybad = s_wt_bad[0] != 0;
-#pragma unroll
-            for (int o = 1; o < WT_WG / 64; ++o) {
-                x = par_compose(x, s_wt_map[o]);
-                anybad |= s_wt_bad[o] != 0;
-            }
-            if (!anybad) r = WideChunk{x.d0, x.d1, x.p, E, 1, 0};
-        }
-        w.chunk[(int64_t) row * w.chunks + c] = r;
+    __syncthreads();
+    WideSeg* out = w.seg + ((int64_t) row * w.chunks + c) * WT_SEGS;
+    if (over) {
+        if (tid == 0) out[0] = WideSeg{0.0, 0.0, 2u, 0, WS_REPLAY, lo, last + 1, 0};
+    } else if (tid < htot) {
+        WideSeg r = s_wt_seg[tid];
+        r.start = s_wt_start[tid];
+        out[tid] = r;
     }
+    if (tid == 0) w.nseg[(int64_t) row * w.chunks + c] = over ? 1 : htot;
+}
+
+__device__ __forceinline__ bool in_binade(double x, int E) {
+    int e;
+    (void) frexp(x, &e);
+    return x >= 0x1p-1000 && x <= 0x1p1000 && e - 1 == E;
 }
 
 // Chain PH of one row from its exact start, with the whole workgroup (uniform control flow): returns the last
@@ -2161,48 +2267,82 @@ __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) 
 template <int PH, typename F>
 __device__ double wt_resolve(const RowsArgs& a, const WideArgs& w, int row, const WtChain<PH>& ch, F stop,
                              int* stopped) {
-    const int tid = (int) threadIdx.x, lane = tid & 63;
+    const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = ch.n, nc = (n + WT_CHUNK - 1) / WT_CHUNK;
     const double* t = wide_terms(a, w, row);
-    const WideChunk* rec = w.chunk + (int64_t) row * w.chunks;
+    const WideSeg* seg = w.seg + (int64_t) row * w.chunks * WT_SEGS;
+    const int32_t* nseg = w.nseg + (int64_t) row * w.chunks;
     double acc = ch.a0;
-    int st = -1, c = 0, wb = -WT_REC;  // wb: the first chunk of the records held in LDS
-    while (c < nc) {
-        if (c >= wb + WT_REC || c + 64 > wb + WT_REC) {  // (re)load the window of records from c on
-            __syncthreads();
-            wb = c;
-            for (int j = tid; j < WT_REC && wb + j < nc; j += TAIL_WG) s_wt_rec[j] = rec[wb + j];
-            __syncthreads();
-        }
-        const WideChunk r0 = s_wt_rec[c - wb];
-        bool in = false;
-        if (r0.mapped) {
-            int E;
-            (void) frexp(acc, &E);
-            in = acc >= 0x1p-1000 && acc <= 0x1p1000 && E - 1 == r0.E;
-        }
-        if (in) {  // (uniform) a run of mapped chunks of r0's binade, at most 64
-            const int cj = c + lane;
-            const WideChunk r = cj < nc ? s_wt_rec[cj - wb] : WideChunk{0.0, 0.0, 2u, 0, 0, 0};
-            const uint64_t run = ballot(cj < nc && r.mapped && r.E == r0.E);
-            const int len = ~run ? (int) __builtin_ctzll(~run) : 64;  // >= 1 (lane 0 is in the run)
-            ParMap x = lane < len ? ParMap{r.d0, r.d1, r.p} : par_identity();
-            x = wave_scan_map<false>(x);
-            const ParMap tot = rdlane_map(x, 63);
-            double A = ldexp(acc, 52 - r0.E);
-            A += dparity(A) ? tot.d1 : tot.d0;
-            if (!(A >= 0x1p52 && A < 0x1p53) && tid == 0) report_fault(a, FAULT_WIDE_MAP);
-            acc = ldexp(A, r0.E - 52);
-            c += len;
-        } else {
-            const int lo = c * WT_CHUNK, len = min(WT_CHUNK, n - lo);
-            int s2;
-            acc = replay_sum<2, WtChain<PH>::NEG>(t + lo, len, acc, stop, &s2);
-            if (s2 >= 0) {
-                st = lo + s2;
-                break;
+    int st = -1;
+    for (int cb = 0; cb < nc && st < 0; cb += WT_WIN) {
+        // the segments of chunks [cb, ce), in order, into LDS
+        const int ce = min(nc, cb + WT_WIN);
+        __syncthreads();
+        if (wave == 0) {
+            const int cnt = cb + lane < ce ? nseg[cb + lane] : 0;
+            int x = cnt;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int y = __shfl_up(x, d, 64);
+                x += lane >= d ? y : 0;
             }
-            ++c;
+            if (lane < WT_WIN) s_wt_off[lane] = x - cnt;
+            if (lane == 63) s_wt_off[WT_WIN] = x;
+        }
+        __syncthreads();
+        const int wn = s_wt_off[WT_WIN];
+        for (int x = tid; x < (ce - cb) * WT_SEGS; x += TAIL_WG) {
+            const int cc = x / WT_SEGS, sg = x - cc * WT_SEGS;
+            if (sg < s_wt_off[cc + 1] - s_wt_off[cc]) s_wt_flat[s_wt_off[cc] + sg] = seg[(int64_t) (cb + cc) * WT_SEGS + sg];
+        }
+        __syncthreads();
+        int i = 0;
+        while (i < wn) {
+            const WideSeg r = s_wt_flat[i];
+            if (r.kind == WS_MAP && in_binade(acc, r.E)) {
+                // a run of mapped segments of r's binade (at most 64): every lane's inclusive composed result
+                const WideSeg q = i + lane < wn ? s_wt_flat[i + lane] : WideSeg{0.0, 0.0, 2u, 0, 0, 0, 0, 0};
+                const uint64_t rm = ballot(i + lane < wn && q.kind == WS_MAP && q.E == r.E);
+                const int len = ~rm ? (int) __builtin_ctzll(~rm) : 64;  // >= 1
+                ParMap x = lane < len ? ParMap{q.d0, q.d1, q.p} : par_identity();
+                x = wave_scan_map<false>(x);
+                const double A = ldexp(acc, 52 - r.E);
+                const double Al = A + (dparity(A) ? x.d1 : x.d0);
+                const double accl = ldexp(Al, r.E - 52);
+                if (ballot(lane < len && !(Al >= 0x1p52 && Al < 0x1p53)) && tid == 0) report_fault(a, FAULT_WIDE_MAP);
+                const uint64_t hit = ballot(lane < len && stop(accl, 0));
+                if (!hit) {
+                    acc = rdlaned(accl, len - 1);
+                    i += len;
+                    continue;
+                }
+                // the stop lies in segment l of the run: replay it from the result before it
+                const int l = (int) __builtin_ctzll(hit);
+                const double from = rdlaned(accl, l > 0 ? l - 1 : 0);
+                const WideSeg h = s_wt_flat[i + l];
+                int s2;
+                acc = replay_sum<2, WtChain<PH>::NEG>(t + h.start, h.end - h.start, l > 0 ? from : acc, stop, &s2);
+                if (s2 >= 0) {
+                    st = h.start + s2;
+                    break;
+                }
+                i += l + 1;
+            } else if (r.kind == WS_TERM) {
+                acc = __dadd_rn(acc, r.d0);
+                if (stop(acc, r.start)) {
+                    st = r.start;
+                    break;
+                }
+                ++i;
+            } else {  // a segment to replay, or a mapped one entered outside its binade
+                int s2;
+                acc = replay_sum<2, WtChain<PH>::NEG>(t + r.start, r.end - r.start, acc, stop, &s2);
+                if (s2 >= 0) {
+                    st = r.start + s2;
+                    break;
+                }
+                ++i;
+            }
         }
     }
     *stopped = st;
