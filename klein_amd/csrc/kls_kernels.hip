@@ -1971,8 +1971,8 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
 // Chunk kernels: WT_WG threads, WT_PT terms each (i = lo + q * WT_WG + tid for the term passes; consecutive
 // runs lo + tid * WT_PT + q where maps are composed in order).
 constexpr int WT_WG = 256, WT_PT = WT_CHUNK / WT_WG;
-constexpr int WT_WIN = 48;  // chunks whose segments a resolve kernel holds in LDS at once
-static_assert(WT_WIN <= 64, "one wave scans the window's segment counts");
+constexpr int WT_FLAT = 1400;  // segment records a resolve kernel holds in LDS at once
+static_assert(WT_FLAT >= WT_SEGS, "a window holds at least one chunk's segments");
 static_assert(WT_CHUNK == 2 * TAIL_WG, "a replayed segment is at most one replay_sum block of two terms per thread");
 // segment codes of a term on its own / past n or past the stop
 constexpr int CODE_HARD = -0x7fffffff, CODE_NONE = -0x7ffffffe;
@@ -1982,8 +1982,11 @@ __shared__ ParMap s_wt_map[WT_WG / 64];
 __shared__ int s_wt_code[WT_WG / 64], s_wt_head[WT_WG / 64], s_wt_hcnt[WT_WG / 64];
 __shared__ WideSeg s_wt_seg[WT_SEGS];
 __shared__ int s_wt_start[WT_SEGS];
-__shared__ WideSeg s_wt_flat[WT_WIN * WT_SEGS];
-__shared__ int s_wt_off[WT_WIN + 1];
+__shared__ WideSeg s_wt_flat[WT_FLAT];
+__shared__ double s_wt_acc;                               // the resolve walk's state, handed between waves
+__shared__ int s_wt_i, s_wt_st, s_wt_rs, s_wt_re;
+__shared__ int s_wt_off[TAIL_WG + 1];
+__shared__ int s_wt_wsum[TAIL_WG / 64];
 
 // Composition for a segmented scan: bit 2 of p marks a map that starts a segment (nothing before it applies).
 __device__ __forceinline__ ParMap seg_compose(const ParMap& e, const ParMap& l) {
@@ -2274,74 +2277,99 @@ __device__ double wt_resolve(const RowsArgs& a, const WideArgs& w, int row, cons
     const int32_t* nseg = w.nseg + (int64_t) row * w.chunks;
     double acc = ch.a0;
     int st = -1;
-    for (int cb = 0; cb < nc && st < 0; cb += WT_WIN) {
-        // the segments of chunks [cb, ce), in order, into LDS
-        const int ce = min(nc, cb + WT_WIN);
+    for (int cb = 0; cb < nc && st < 0;) {
+        // a window of chunks [cb, ce) whose segments fit in LDS: the segment counts of up to TAIL_WG chunks,
+        // scanned (s_wt_off: the chunks' first records), then as many chunks as fit (at least one)
         __syncthreads();
-        if (wave == 0) {
-            const int cnt = cb + lane < ce ? nseg[cb + lane] : 0;
-            int x = cnt;
+        const int cnt = cb + tid < nc ? nseg[cb + tid] : 0;
+        int cs = cnt;  // inclusive scan of the counts
 #pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const int y = __shfl_up(x, d, 64);
-                x += lane >= d ? y : 0;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(cs, d, 64);
+            cs += lane >= d ? y : 0;
+        }
+        if (lane == 63) s_wt_wsum[wave] = cs;
+        __syncthreads();
+#pragma unroll
+        for (int o = 0; o < TAIL_WG / 64; ++o) cs += o < wave ? s_wt_wsum[o] : 0;
+        s_wt_off[tid + 1] = cs;
+        if (tid == 0) s_wt_off[0] = 0;
+        const int fit = __syncthreads_count(cb + tid < nc && cs <= WT_FLAT);
+        const int ce = cb + max(fit, 1), wn = s_wt_off[ce - cb];
+        for (int r = tid; r < wn; r += TAIL_WG) {
+            int lo_c = 0, hi_c = ce - cb - 1;  // the chunk of record r: the last cc with s_wt_off[cc] <= r
+            while (lo_c < hi_c) {
+                const int mid = (lo_c + hi_c + 1) >> 1;
+                if (s_wt_off[mid] <= r) lo_c = mid;
+                else hi_c = mid - 1;
             }
-            if (lane < WT_WIN) s_wt_off[lane] = x - cnt;
-            if (lane == 63) s_wt_off[WT_WIN] = x;
+            s_wt_flat[r] = seg[(int64_t) (cb + lo_c) * WT_SEGS + (r - s_wt_off[lo_c])];
         }
         __syncthreads();
-        const int wn = s_wt_off[WT_WIN];
-        for (int x = tid; x < (ce - cb) * WT_SEGS; x += TAIL_WG) {
-            const int cc = x / WT_SEGS, sg = x - cc * WT_SEGS;
-            if (sg < s_wt_off[cc + 1] - s_wt_off[cc]) s_wt_flat[s_wt_off[cc] + sg] = seg[(int64_t) (cb + cc) * WT_SEGS + sg];
-        }
-        __syncthreads();
+        cb = ce;
+        // wave 0 walks the window's records; the workgroup joins it for a replay (replay_sum)
         int i = 0;
-        while (i < wn) {
-            const WideSeg r = s_wt_flat[i];
-            if (r.kind == WS_MAP && in_binade(acc, r.E)) {
-                // a run of mapped segments of r's binade (at most 64): every lane's inclusive composed result
-                const WideSeg q = i + lane < wn ? s_wt_flat[i + lane] : WideSeg{0.0, 0.0, 2u, 0, 0, 0, 0, 0};
-                const uint64_t rm = ballot(i + lane < wn && q.kind == WS_MAP && q.E == r.E);
-                const int len = ~rm ? (int) __builtin_ctzll(~rm) : 64;  // >= 1
-                ParMap x = lane < len ? ParMap{q.d0, q.d1, q.p} : par_identity();
-                x = wave_scan_map<false>(x);
-                const double A = ldexp(acc, 52 - r.E);
-                const double Al = A + (dparity(A) ? x.d1 : x.d0);
-                const double accl = ldexp(Al, r.E - 52);
-                if (ballot(lane < len && !(Al >= 0x1p52 && Al < 0x1p53)) && tid == 0) report_fault(a, FAULT_WIDE_MAP);
-                const uint64_t hit = ballot(lane < len && stop(accl, 0));
-                if (!hit) {
-                    acc = rdlaned(accl, len - 1);
-                    i += len;
-                    continue;
+        while (true) {  // (uniform)
+            if (wave == 0) {
+                int rs = -1, re = -1;
+                while (i < wn && st < 0) {
+                    const WideSeg r = s_wt_flat[i];
+                    if (r.kind == WS_MAP && in_binade(acc, r.E)) {
+                        // a run of mapped segments of r's binade (at most 64): each lane's inclusive result
+                        const WideSeg q = i + lane < wn ? s_wt_flat[i + lane] : WideSeg{0.0, 0.0, 2u, 0, 0, 0, 0, 0};
+                        const uint64_t rm = ballot(i + lane < wn && q.kind == WS_MAP && q.E == r.E);
+                        const int len = ~rm ? (int) __builtin_ctzll(~rm) : 64;  // >= 1
+                        ParMap x = lane < len ? ParMap{q.d0, q.d1, q.p} : par_identity();
+                        if (len > 1) x = wave_scan_map<false>(x);
+                        const double A = ldexp(acc, 52 - r.E);
+                        const double Al = A + (dparity(A) ? x.d1 : x.d0);
+                        const double accl = ldexp(Al, r.E - 52);
+                        if (ballot(lane < len && !(Al >= 0x1p52 && Al < 0x1p53)) && lane == 0) report_fault(a, FAULT_WIDE_MAP);
+                        const uint64_t hit = ballot(lane < len && stop(accl, 0));
+                        if (!hit) {
+                            acc = rdlaned(accl, len - 1);
+                            i += len;
+                            continue;
+                        }
+                        // the stop lies in segment l of the run: replay it from the result before it
+                        const int l = (int) __builtin_ctzll(hit);
+                        const WideSeg h = s_wt_flat[i + l];
+                        acc = l > 0 ? rdlaned(accl, l - 1) : acc;
+                        rs = h.start;
+                        re = h.end;
+                        i += l + 1;
+                        break;
+                    } else if (r.kind == WS_TERM) {
+                        acc = __dadd_rn(acc, r.d0);
+                        if (stop(acc, r.start)) st = r.start;
+                        ++i;
+                    } else {  // a segment to replay, or a mapped one entered outside its binade
+                        rs = r.start;
+                        re = r.end;
+                        ++i;
+                        break;
+                    }
                 }
-                // the stop lies in segment l of the run: replay it from the result before it
-                const int l = (int) __builtin_ctzll(hit);
-                const double from = rdlaned(accl, l > 0 ? l - 1 : 0);
-                const WideSeg h = s_wt_flat[i + l];
-                int s2;
-                acc = replay_sum<2, WtChain<PH>::NEG>(t + h.start, h.end - h.start, l > 0 ? from : acc, stop, &s2);
-                if (s2 >= 0) {
-                    st = h.start + s2;
-                    break;
+                if (lane == 0) {
+                    s_wt_acc = acc;
+                    s_wt_i = i;
+                    s_wt_st = st;
+                    s_wt_rs = rs;
+                    s_wt_re = re;
                 }
-                i += l + 1;
-            } else if (r.kind == WS_TERM) {
-                acc = __dadd_rn(acc, r.d0);
-                if (stop(acc, r.start)) {
-                    st = r.start;
-                    break;
-                }
-                ++i;
-            } else {  // a segment to replay, or a mapped one entered outside its binade
-                int s2;
-                acc = replay_sum<2, WtChain<PH>::NEG>(t + r.start, r.end - r.start, acc, stop, &s2);
-                if (s2 >= 0) {
-                    st = r.start + s2;
-                    break;
-                }
-                ++i;
+            }
+            __syncthreads();
+            acc = s_wt_acc;
+            i = s_wt_i;
+            st = s_wt_st;
+            const int rs = s_wt_rs, re = s_wt_re;
+            __syncthreads();  // (read before wave 0 rewrites them)
+            if (rs < 0) break;  // the window is walked, or the chain stopped
+            int s2;
+            acc = replay_sum<2, WtChain<PH>::NEG>(t + rs, re - rs, acc, stop, &s2);
+            if (s2 >= 0) {
+                st = rs + s2;
+                break;
             }
         }
     }

@@ -1,10 +1,10 @@
 // Device-wide descending sort of 64-bit keys for the wide top-k path: a stable least-significant-digit radix sort,
-// 8 bits per pass, three kernels per pass (no memset, so a pass can be captured in a graph):
-//   1. sort_hist_kernel: each tile of SORT_TILE keys counts its digits in LDS, written digit-major:
-//      counts[digit * tiles + tile];
-//   2. sort_scan_kernel: one workgroup turns the counts into an exclusive scan in place (digit-major order, so
-//      digit d of tile t starts after every smaller digit and after digit d of every earlier tile);
-//   3. sort_scatter_kernel: each tile ranks its keys stably and writes them to their slots.
+// 8 bits per pass, two kernels per pass (no memset, so a pass can be captured in a graph):
+//   1. sort_hist_kernel: each tile of SORT_TILE keys counts its digits in LDS, written tile-major:
+//      counts[tile * 256 + digit];
+//   2. sort_scatter_kernel: each tile finds where its keys of each digit start (the keys of smaller digits in all
+//      tiles, then those of its digit in earlier tiles: sums over the count table, read coalesced by four groups
+//      of 256 threads, and a scan over the 256 digit totals in LDS), ranks its keys stably and writes them there.
 // Descending order is ascending order of the inverted digit (255 - digit). Within a tile, key i of the tile is
 // held by wave i / 512, slot (i / 64) % 8, lane i % 64; a wave ranks its 512 keys slot by slot: the lanes of a
 // slot whose digits are equal are found with eight ballots, a key's rank is the wave's count of that digit so far
@@ -29,7 +29,7 @@ __device__ __forceinline__ size_t tile_index(unsigned tile, int wave, int s, int
 }
 
 __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __restrict__ in, uint32_t n, int shift,
-                                                          uint32_t tiles, uint32_t* __restrict__ counts) {
+                                                          uint32_t* __restrict__ counts) {
     __shared__ uint32_t h[256];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < 256) h[tid] = 0u;
@@ -40,76 +40,73 @@ __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __rest
         if (i < n) atomicAdd(&h[rdigit(in[i], shift)], 1u);
     }
     __syncthreads();
-    if (tid < 256) counts[(size_t) tid * tiles + blockIdx.x] = h[tid];
+    if (tid < 256) counts[(size_t) blockIdx.x * 256 + tid] = h[tid];
 }
 
-// Exclusive scan of counts[0..m) in place, one workgroup: thread t takes a contiguous run of c = ceil(m / ST_WG)
-// entries. Runs of up to SCAN_REG entries are loaded into registers at once (every load in flight together);
-// longer ones (grids of more than 128 tiles) are read twice in loops.
-constexpr int SCAN_REG = 32;
-
-__global__ __launch_bounds__(ST_WG) void sort_scan_kernel(uint32_t* __restrict__ counts, uint32_t m) {
-    __shared__ uint32_t ws[ST_NW];
-    const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t c = (m + ST_WG - 1) / ST_WG;
-    const uint32_t lo = min(m, (uint32_t) tid * c), hi = min(m, lo + c);
-    const bool reg = c <= SCAN_REG;  // (uniform)
-    uint32_t v[SCAN_REG];
-    uint32_t sum = 0u;
-    if (reg) {
-#pragma unroll
-        for (int j = 0; j < SCAN_REG; ++j) v[j] = lo + j < hi ? counts[lo + j] : 0u;
-#pragma unroll
-        for (int j = 0; j < SCAN_REG; ++j) sum += v[j];
-    } else {
-        for (uint32_t i = lo; i < hi; ++i) sum += counts[i];
-    }
-    uint32_t x = sum;  // inclusive scan across the wave
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t y = (uint32_t) __shfl_up((int) x, (unsigned) d, 64);
-        x += lane >= d ? y : 0u;
-    }
-    if (lane == 63) ws[wave] = x;
-    __syncthreads();
-    uint32_t run = x - sum;
-#pragma unroll
-    for (int w = 0; w < ST_NW; ++w) run += w < wave ? ws[w] : 0u;
-    if (reg) {
-#pragma unroll
-        for (int j = 0; j < SCAN_REG; ++j) {
-            if (lo + j < hi) counts[lo + j] = run;
-            run += v[j];
-        }
-    } else {
-        for (uint32_t i = lo; i < hi; ++i) {
-            const uint32_t y = counts[i];
-            counts[i] = run;
-            run += y;
-        }
-    }
-}
+constexpr int SC_UNROLL = 8;  // count-table rows in flight per thread
 
 __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
                                                              uint32_t n, int shift, uint32_t tiles,
-                                                             const uint32_t* __restrict__ offs) {
+                                                             const uint32_t* __restrict__ counts) {
     __shared__ uint32_t cw[ST_NW][256];  // per wave: digit counts so far, then the earlier waves' counts
     __shared__ uint32_t tb[256];         // this tile's first slot per digit
+    __shared__ uint32_t part[2][4][256];  // the count sums of the four groups: earlier tiles, all tiles
+    __shared__ uint32_t wsum[4];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < ST_NW * 256; i += ST_WG) (&cw[0][0])[i] = 0u;
-    if (tid < 256) tb[tid] = offs[(size_t) tid * tiles + blockIdx.x];
+    const uint32_t tile = blockIdx.x;
     uint64_t k[ST_PER];
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
-        const size_t i = tile_index(blockIdx.x, wave, s, lane);
+        const size_t i = tile_index(tile, wave, s, lane);
         k[s] = i < n ? in[i] : 0ull;
     }
+    for (int i = tid; i < ST_NW * 256; i += ST_WG) (&cw[0][0])[i] = 0u;
+    {
+        // group g sums rows g, g + 4, ... of the count table for digit d
+        const int g = tid >> 8, d = tid & 255;
+        uint32_t before = 0u, all = 0u;
+        for (uint32_t t0 = (uint32_t) g; t0 < tiles; t0 += 4 * SC_UNROLL) {
+            uint32_t v[SC_UNROLL];
+#pragma unroll
+            for (int u = 0; u < SC_UNROLL; ++u) {
+                const uint32_t t = t0 + 4u * u;
+                v[u] = t < tiles ? counts[(size_t) t * 256 + d] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < SC_UNROLL; ++u) {
+                all += v[u];
+                before += t0 + 4u * u < tile ? v[u] : 0u;
+            }
+        }
+        part[0][g][d] = before;
+        part[1][g][d] = all;
+    }
     __syncthreads();
+    if (tid < 256) {
+        // digit totals over every tile, scanned over the digits (4 waves of 64); plus the earlier tiles' counts
+        const uint32_t before = part[0][0][tid] + part[0][1][tid] + part[0][2][tid] + part[0][3][tid];
+        const uint32_t all = part[1][0][tid] + part[1][1][tid] + part[1][2][tid] + part[1][3][tid];
+        uint32_t x = all;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t y = (uint32_t) __shfl_up((int) x, (unsigned) d, 64);
+            x += lane >= d ? y : 0u;
+        }
+        if (lane == 63) wsum[wave] = x;
+        tb[tid] = x - all + before;  // (the earlier waves' totals are added below)
+    }
+    __syncthreads();
+    if (tid < 256) {
+        uint32_t add = 0u;
+#pragma unroll
+        for (int w = 0; w < 3; ++w) add += w < wave ? wsum[w] : 0u;
+        tb[tid] += add;
+    }
     const uint64_t below = (1ull << lane) - 1ull;
     uint32_t rk[ST_PER];
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
-        const bool valid = tile_index(blockIdx.x, wave, s, lane) < n;
+        const bool valid = tile_index(tile, wave, s, lane) < n;
         const uint32_t d = rdigit(k[s], shift);
         uint64_t same = ballot64(valid);  // (all lanes take part in every ballot)
 #pragma unroll
@@ -136,7 +133,7 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
-        if (tile_index(blockIdx.x, wave, s, lane) < n) {
+        if (tile_index(tile, wave, s, lane) < n) {
             const uint32_t d = rdigit(k[s], shift);
             const uint32_t pos = tb[d] + cw[wave][d] + rk[s];
             if (pos < n) out[pos] = k[s];  // (always: the counts are the tile's own)
@@ -154,8 +151,7 @@ hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int begin_bit, int
     uint64_t* src = a;
     uint64_t* dst = b;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
-        hipLaunchKernelGGL(sort_hist_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, (uint32_t) n, shift, tiles, counts);
-        hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(ST_WG), 0, s, counts, 256u * tiles);
+        hipLaunchKernelGGL(sort_hist_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, (uint32_t) n, shift, counts);
         hipLaunchKernelGGL(sort_scatter_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, dst, (uint32_t) n, shift, tiles,
                            counts);
         const hipError_t e = hipGetLastError();

@@ -119,7 +119,8 @@ def test_wide_batch(torch_cuda, K, oracle_lib, case):
 
 # The wide tail's chunked chains: rows whose sums cross many binades over many chunks (flat logits), top-p at 1
 # (no stop), min-p cutting inside a chunk, a k that ends inside a chunk, bf16-valued rows (runs of equal terms),
-# low and high temperatures, and uniforms 0 and 0.9999999 (the draw stopping at once / running to the end).
+# low and high temperatures, uniforms 0.9999999 and 0 (the draw running to the end / stopping at once), and a
+# 3,000,000-entry vocabulary (1,465 chunks: the resolve kernels' segment records in several windows).
 # V, rows, temperature, top_k, top_p, min_p, kind
 CHUNK_CASES = [
     (248320, 3, 1.0, 0, 0.95, 0.0, "flat"),
@@ -128,6 +129,7 @@ CHUNK_CASES = [
     (248320, 3, 1.0, 5000, 0.99, 0.0, "heads"),
     (248320, 3, 1.0, 0, 0.95, 0.0, "bf16"),
     (65536, 3, 3.0, 0, 0.999, 0.0, "flat"),
+    (3000000, 1, 1.0, 0, 0.999, 0.0, "flat"),
 ]
 
 
@@ -144,7 +146,7 @@ def test_wide_chunked_chains(torch_cuda, K, oracle_lib, case):
         if kind == "bf16":
             x = (x.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
     p = W.Params(temperature=T, top_k=k, top_p=tp, min_p=mp)
-    u = np.array([0.0, 0.9999999, rng.random()])
+    u = np.array([0.9999999, 0.0, rng.random()])[:rows]
     S = K.Sampler(p, n_vocab=V, max_rows=rows)
     assert S.path == "wide", (case, S.path)
     out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
