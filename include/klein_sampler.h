@@ -55,9 +55,10 @@ typedef void* kls_stream;
  * max_rows bounds the rows of kls_verify and kls_sample_batch. A top-k of 65 to 1024 takes the mid path: one
  * kernel, like top-k <= 64, with a 128 KB candidate buffer per row (vocabularies of up to 16384 / top_k segments
  * of 32768 ids: n_vocab <= 524,288 for every such top-k). A larger top-k (or no limit) takes a slower path
- * that keys and sorts every logit of a row (2 x 8 bytes per logit per row of device memory; a key kernel, a radix
- * sort's passes and a tail kernel, captured together in a verify step's graph); it needs n_vocab * max_rows below
- * 2^32 (KLS_ERR_UNSUPPORTED otherwise). */
+ * that keys and sorts every logit of a row (2 x 8 bytes per logit per row of device memory, plus ~2.6 KB per
+ * 2,048 ids per row for the tail's chunk records; a key kernel, a radix sort's passes and the tail's kernels,
+ * captured together in a verify step's graph); it needs n_vocab * max_rows below 2^32 (KLS_ERR_UNSUPPORTED
+ * otherwise). */
 int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* out);
 
 int kls_destroy(kls_handle h);
@@ -244,7 +245,8 @@ enum kls_path { KLS_PATH_FAST = 0, KLS_PATH_MID = 1, KLS_PATH_WIDE = 2 };
 int kls_debug_path(kls_handle h, int32_t* out_path);
 
 /* Test hook, no counterpart in the reference: the wide top-k tail's parallel replay of a sequential double sum
- * (src/sampler.cpp:58,70-77,84-87 accumulate this way) over the n device doubles d_terms from acc0:
+ * (src/sampler.cpp:58,70-77,84-87 accumulate this way; the block form that replays the wide tail's segments and
+ * the mid path's tail) over the n device doubles d_terms from acc0:
  * acc = acc + d_terms[i] in order, stopping after the first i where (mode 1) acc >= thr or (mode 2) acc <= 0
  * (mode 0: never). d_out[0] receives the result, d_out[1] the stop index (-1: none). Asynchronous on `stream`. */
 int kls_debug_sum_replay(const double* d_terms, int n, double acc0, int mode, double thr, double* d_out,
