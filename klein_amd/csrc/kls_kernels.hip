@@ -2384,6 +2384,8 @@ __global__ __launch_bounds__(TAIL_WG) void wt_resolve_kernel(RowsArgs a, WideArg
     const int row = (int) blockIdx.x, tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
     WideRow* rs = w.rowst + row;
     const WtChain<PH> ch(a, *rs);
+    // the call block (pinned host memory) read at the start: its round trip overlaps the chain's first loads
+    const CallIn cin = PH > 0 ? read_call<false>(a, row) : CallIn{0u, -1, 0.0};
     int st = -1;
     double acc = ch.a0;
     if (ch.n > 0) {
@@ -2403,7 +2405,7 @@ __global__ __launch_bounds__(TAIL_WG) void wt_resolve_kernel(RowsArgs a, WideArg
     } else if (PH == 1) {
         // top-p (:70-79) keeps up to the stop; the draw's total (:80-81) is the chain's result there
         const int n_top = st >= 0 ? st + 1 : ch.n;
-        const double u = read_call<false>(a, row).u;
+        const double u = cin.u;
         rs->n_top = n_top;
         rs->total = acc;
         rs->r0 = __dadd_rn(__dmul_rn(u, __dsub_rn(acc, 0.0)), 0.0);
@@ -2412,7 +2414,6 @@ __global__ __launch_bounds__(TAIL_WG) void wt_resolve_kernel(RowsArgs a, WideArg
         const WideKeyFmt fmt = wide_fmt(w);
         const uint64_t* K = w.sorted + (int64_t) row * a.V;
         const int kk = rs->kk, n_top = ch.n;
-        const CallIn cin = read_call<false>(a, row);
         const int idx = st >= 0 ? st : n_top - 1;
         const int tok = kk > 0 ? fmt.id(K[idx]) : 0;  // no number in the row: the fast path's empty list
         const bool act = lane < kk;
@@ -2622,6 +2623,10 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
             for (int e = 0; e < 4; ++e) v[4 * i + e] = b + e < hi ? L[b + e] : __uint_as_float(0x7fc00000u);
         }
     }
+    // what the row's last workgroup needs from the call block (pinned host memory for graph-replayed steps), read
+    // by every workgroup once its logit loads are issued: the PCIe round trip then ends before the first barrier
+    // (which comes after the logits) instead of holding the last workgroup's first wait
+    const CallIn cin = read_call<false>(a, row);
     if (PENALIZE) {
         RawHistory rh;
         if (a.hist_off) {
@@ -2701,7 +2706,6 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
     if (!s_last) return;
 
     // ---- the row's last workgroup
-    const CallIn cin = read_call<false>(a, row);
     if (tid == 0)
         s_mid_base = (int) __hip_atomic_exchange(&m.fill[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
