@@ -221,7 +221,9 @@ int kls_debug_expf(uint32_t lo, long long n, float* d_out, kls_stream stream);
  * which workgroups of a row share a running bound through device memory, xcd_map = 1 to deal a row's segments
  * to one XCD, 0 for plain order. Results do not depend on the layout; tests use it to reach every code path.
  * wait_limit bounds the polls of the kernels' internal waits (0: the default, 2^20; negative: none, so such a
- * wait gives up at once and the call reports KLS_ERR_HIP): tests force the failure path with it. */
+ * wait gives up at once and the call reports KLS_ERR_HIP): tests force the failure path with it. wide_segs caps
+ * the segments a chunk of the wide top-k tail may leave (0: the default, 64; else 1..64): a chunk of more is
+ * replayed term by term, which tests reach with it. */
 typedef struct kls_debug_layout {
     int32_t seg_len;
     int32_t target_wg;
@@ -229,6 +231,7 @@ typedef struct kls_debug_layout {
     int32_t share_min_wg;
     int32_t xcd_map;
     int32_t wait_limit;
+    int32_t wide_segs;
 } kls_debug_layout;
 int kls_debug_set_layout(kls_handle h, const kls_debug_layout* layout);
 

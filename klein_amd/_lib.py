@@ -33,7 +33,8 @@ class KlsParams(C.Structure):
 
 class KlsDebugLayout(C.Structure):
     _fields_ = [("seg_len", C.c_int32), ("target_wg", C.c_int32), ("wide_target_wg", C.c_int32),
-                ("share_min_wg", C.c_int32), ("xcd_map", C.c_int32), ("wait_limit", C.c_int32)]
+                ("share_min_wg", C.c_int32), ("xcd_map", C.c_int32), ("wait_limit", C.c_int32),
+                ("wide_segs", C.c_int32)]
 
 
 class KlsRecurrentDesc(C.Structure):

@@ -607,6 +607,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
         ALLOC(h->w.sorted, sizeof(uint64_t) * R * n_vocab);
         ALLOC(h->w.counts, sizeof(uint32_t) * 256 * sort_tiles(R * (size_t) n_vocab));
         h->w.chunks = (k + WT_CHUNK - 1) / WT_CHUNK;
+        h->w.seg_cap = WT_SEGS;
         ALLOC(h->w.part, sizeof(double) * R * h->w.chunks);
         ALLOC(h->w.seg, sizeof(WideSeg) * R * h->w.chunks * WT_SEGS);
         ALLOC(h->w.nseg, sizeof(int32_t) * R * h->w.chunks);
@@ -729,7 +730,8 @@ int kls_debug_set_layout(kls_handle h, const kls_debug_layout* l) {
     const int o = l->seg_len;
     if (o != 0 && (o < SEG_MIN || o > SEG_MAX || (o & (o - 1)) != 0))
         return fail(KLS_ERR_INVALID_ARG, "segment length must be 0 or a power of two in [1024, 65536]");
-    if (l->target_wg < 0 || l->wide_target_wg < 0 || l->share_min_wg < 0 || l->xcd_map < -1 || l->xcd_map > 1)
+    if (l->target_wg < 0 || l->wide_target_wg < 0 || l->share_min_wg < 0 || l->xcd_map < -1 || l->xcd_map > 1 ||
+        l->wide_segs < 0 || l->wide_segs > WT_SEGS)
         return fail(KLS_ERR_INVALID_ARG, "layout field out of range");
     h->seg_len_override = o;
     if (l->target_wg) h->target_wg = l->target_wg;
@@ -737,6 +739,7 @@ int kls_debug_set_layout(kls_handle h, const kls_debug_layout* l) {
     if (l->share_min_wg) h->share_min_wg = l->share_min_wg;
     if (l->xcd_map >= 0) h->xcd_map = l->xcd_map;
     h->spin_limit = l->wait_limit == 0 ? DEFAULT_SPIN_LIMIT : l->wait_limit < 0 ? 0 : l->wait_limit;
+    h->w.seg_cap = l->wide_segs == 0 ? WT_SEGS : l->wide_segs;
     h->g_valid = false;  // (the verify graph bakes the layout in)
     return KLS_OK;
 }

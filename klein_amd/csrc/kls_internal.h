@@ -160,6 +160,7 @@ struct WideArgs {
     int32_t k;            // MID_KMAX < k <= V (or a k the mid path cannot hold)
     int32_t id_bits;      // ids are below 1 << id_bits
     int32_t chunks;       // chunks per row: ceil(k / WT_CHUNK)
+    int32_t seg_cap;      // segments a chunk may leave (WT_SEGS; fewer only under a test layout)
     double* part;         // [max_rows * chunks] term sums of the chunks
     WideSeg* seg;         // [max_rows * chunks * WT_SEGS] the chunks' segments of the chain being resolved
     int32_t* nseg;        // [max_rows * chunks] segments per chunk

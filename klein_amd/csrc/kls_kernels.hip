@@ -2216,7 +2216,7 @@ __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) 
         htot += v;
         if (o < wave) win = seg_compose(win, s_wt_map[o]);
     }
-    const bool over = htot > WT_SEGS;  // (uniform)
+    const bool over = htot > w.seg_cap;  // (uniform)
     if (!over) {
         // each segment's record at its last term (its start at its head)
         ParMap R = seg_compose(win, te);

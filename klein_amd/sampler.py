@@ -85,10 +85,11 @@ class Sampler:
             _lib.check(L.kls_accept(self._h, int(t)), "kls_accept")
         self._early = []
 
-    def set_layout(self, seg_len=0, target_wg=0, wide_target_wg=0, share_min_wg=0, xcd_map=-1, wait_limit=0):
+    def set_layout(self, seg_len=0, target_wg=0, wide_target_wg=0, share_min_wg=0, xcd_map=-1, wait_limit=0,
+                   wide_segs=0):
         """Test hook (kls_debug_set_layout): a field of 0 (xcd_map -1) keeps the default."""
         lay = _lib.KlsDebugLayout(int(seg_len), int(target_wg), int(wide_target_wg), int(share_min_wg), int(xcd_map),
-                                  int(wait_limit))
+                                  int(wait_limit), int(wide_segs))
         _lib.check(_lib.lib().kls_debug_set_layout(self._h, C.byref(lay)), "kls_debug_set_layout")
 
     def device_results(self):

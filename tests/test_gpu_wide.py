@@ -161,6 +161,32 @@ def test_wide_chunked_chains(torch_cuda, K, oracle_lib, case):
     S.close()
 
 
+@pytest.mark.parametrize("case,cap", [(0, 1), (2, 3), (3, 2)])
+def test_wide_chunks_replayed(torch_cuda, K, oracle_lib, case, cap):
+    """The wide tail with at most `cap` segments per chunk (a test layout): chunks with more (the start, binade
+    crossings, the stops) are replayed term by term between mapped chunks and single terms."""
+    torch = torch_cuda
+    O = oracle_lib
+    V, rows, T, k, tp, mp, kind = CHUNK_CASES[case]
+    rng = np.random.default_rng(1800 + case)
+    x = head_rows(rng, rows, V) if kind == "heads" else (rng.standard_normal((rows, V)) * 1.5).astype(np.float32)
+    p = W.Params(temperature=T, top_k=k, top_p=tp, min_p=mp)
+    u = np.array([0.9999999, 0.0, rng.random()])[:rows]
+    S = K.Sampler(p, n_vocab=V, max_rows=rows)
+    assert S.path == "wide", (case, S.path)
+    S.set_layout(wide_segs=cap)
+    out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    say("wide chunks replayed", case, "cap", cap)
+    S.sample_batch(dev(torch, x), dev(torch, u), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        t = check_row(S, O, x[r], p, u[r], None, r, f"replayed{case}")
+        assert got[r] == t, (case, r, got[r], t)
+    S.check()
+    S.close()
+
+
 def test_wide_ties_and_infinities(torch_cuda, K, oracle_lib):
     """Every logit equal (candidate order is id order), and rows with -inf logits, under no top-k limit."""
     torch = torch_cuda
