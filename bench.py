@@ -415,16 +415,26 @@ def main():
         _lib.check(L.kls_verify(h, dptr, 4, dr_p, u_ps[i], exp_t[i].ctypes.data_as(I32P), C.byref(acc1), sp),
                    "kls_verify")
         exp_a[i] = acc1.value
-    n_rec = max(a.steps, a.warmup, 1000 if not a.no_extra else 1)
+    n_rec = max(a.steps, a.warmup, 1000 if not a.no_extra else 1, 200)
     rec_t = np.zeros((n_rec, 4), np.int32)
     rec_a = np.zeros(n_rec, np.int32)
     rec_tp = [rec_t[i].ctypes.data_as(I32P) for i in range(n_rec)]
     rec_ap = [C.cast(rec_a.ctypes.data + 4 * i, I32P) for i in range(n_rec)]
 
-    def step(i, j):
-        st = L.kls_verify(h, dptr, 4, dr_p, u_ps[i % M], rec_tp[j], rec_ap[j], sp)
-        if st:
-            _lib.check(st, "kls_verify")
+    # The timed steps run back to back from C (kls_debug_run_verify_steps: one kls_verify per step, as klein's C++
+    # generation loop calls the sampler), so no Python call sits between steps; each step's host wall time
+    # (enqueue to tokens on the host) comes back per step, and every step's tokens are checked afterwards.
+    I64P = C.POINTER(C.c_int64)
+    dr_all = np.ascontiguousarray(np.tile(drafts, (n_rec, 1)), dtype=np.int32)
+    step_ns = np.zeros(n_rec, np.int64)
+
+    def run_steps(n, first):
+        """Steps first .. first+n-1 (uniform set i % M) into rec_t / rec_a [0, n); returns their ns."""
+        u_all = np.ascontiguousarray(us[(np.arange(first, first + n)) % M], dtype=np.float64)
+        _lib.check(L.kls_debug_run_verify_steps(h, dptr, 4, n, dr_all.ctypes.data_as(I32P), u_all.ctypes.data_as(F64P),
+                                                rec_t.ctypes.data_as(I32P), rec_a.ctypes.data_as(I32P),
+                                                step_ns.ctypes.data_as(I64P), sp), "kls_debug_run_verify_steps")
+        return step_ns[:n].copy()
 
     def check_steps(n, first):
         for j in range(n):
@@ -433,42 +443,40 @@ def main():
             assert acc == exp_a[i % M] and list(rec_t[j][:acc + 1]) == list(exp_t[i % M][:acc + 1]), \
                 f"step {i}: tokens differ from the untimed launch"
 
-    for i in range(a.warmup):
-        step(i, i)
+    run_steps(a.warmup, 0)
     check_steps(a.warmup, 0)
     torch.cuda.synchronize()
-    ts = [0] * (a.steps + 1)
-    pc = time.perf_counter_ns
     t0 = time.perf_counter()
-    ts[0] = pc()
-    for i in range(a.steps):
-        step(i, i)
-        ts[i + 1] = pc()
+    ns = run_steps(a.steps, 0)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     us_step = (t1 - t0) / a.steps * 1e6
     check_steps(a.steps, 0)
-    per = [(ts[i + 1] - ts[i]) / 1e3 for i in range(a.steps)]
+    per = [x / 1e3 for x in ns]
     lat = {"first_25_us": [round(x, 1) for x in per[:25]], "median_us": round(pct(per, 50), 2),
-           "p99_us": round(pct(per, 99), 2), "steps_checked": a.warmup + a.steps}
+           "p99_us": round(pct(per, 99), 2), "steps_checked": a.warmup + a.steps,
+           "loop": "C (kls_debug_run_verify_steps)"}
+    # the same steps called one by one from Python (one ctypes call per step), for comparison
+    pc = time.perf_counter_ns
+    py = []
+    for j in range(200):
+        x0 = pc()
+        _lib.check(L.kls_verify(h, dptr, 4, dr_p, u_ps[j % M], rec_tp[j], rec_ap[j], sp), "kls_verify")
+        py.append((pc() - x0) / 1e3)
+    check_steps(200, 0)
+    lat["python_loop_200"] = {"median_us": round(pct(py, 50), 2), "mean_us": round(sum(py) / len(py), 2)}
 
     if not a.no_extra:
         # 1,000 more steps (hot), then 200 with the last-level cache flushed between steps (cold HBM)
-        hot = []
-        for j in range(1000):
-            x0 = pc()
-            step(j, j)
-            hot.append((pc() - x0) / 1e3)
+        hot = [x / 1e3 for x in run_steps(1000, 0)]
         check_steps(1000, 0)
         flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device="cuda")
         cold = []
         for j in range(200):
             flush.fill_(float(j))
             torch.cuda.synchronize()
-            x0 = pc()
-            step(j, j)
-            cold.append((pc() - x0) / 1e3)
-        check_steps(200, 0)
+            cold.append(run_steps(1, j)[0] / 1e3)
+            check_steps(1, j)
         del flush
         lat["hot_1000"] = {"median_us": round(pct(hot, 50), 2), "p99_us": round(pct(hot, 99), 2),
                            "mean_us": round(sum(hot) / len(hot), 2)}

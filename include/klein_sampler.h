@@ -242,6 +242,15 @@ int kls_debug_set_layout(kls_handle h, const kls_debug_layout* layout);
  * the handle's results are those of that step again afterwards. */
 int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, double* out_us);
 
+/* Measurement hook, no counterpart in the reference: n_steps verify steps (kls_verify) back to back from C, as a
+ * C++ engine's generation loop calls them (src/engine.cpp:563-575 runs once per step): step i samples the nb
+ * rows at `logits` with drafts[i*(nb-1) ...] and u[i*nb ...] and writes out_tokens[i*nb ...] and
+ * out_accepted[i]; out_step_ns[i] (may be NULL) receives the step's host wall time in nanoseconds (enqueue to
+ * tokens on the host). Stops at the first step that fails and returns its status. */
+int kls_debug_run_verify_steps(kls_handle h, const float* logits, int nb, int n_steps, const int32_t* drafts,
+                               const double* u, int32_t* out_tokens, int32_t* out_accepted, int64_t* out_step_ns,
+                               kls_stream stream);
+
 /* Test hook, no counterpart in the reference: *out_path = the kernel path the handle's sampling calls take
  * (greedy and top-k <= 64: FAST; top-k 65..1024: MID; larger or no limit: WIDE). */
 enum kls_path { KLS_PATH_FAST = 0, KLS_PATH_MID = 1, KLS_PATH_WIDE = 2 };

@@ -21,7 +21,8 @@ KLS_ERR_OOM = 6
 EXPORTS = ["kls_create", "kls_destroy", "kls_reset", "kls_accept", "kls_sample", "kls_verify", "kls_verify_enqueue",
            "kls_verify_wait", "kls_sample_batch", "kls_sample_batch_noalloc", "kls_argmax", "kls_ppl_scores",
            "kls_device_results", "kls_check", "kls_recurrent_create", "kls_recurrent_destroy",
-           "kls_rollback_recurrent", "kls_get_candidates", "kls_debug_set_layout", "kls_debug_time_verify", "kls_debug_path", "kls_debug_expf",
+           "kls_rollback_recurrent", "kls_get_candidates", "kls_debug_set_layout", "kls_debug_time_verify",
+           "kls_debug_run_verify_steps", "kls_debug_path", "kls_debug_expf",
            "kls_debug_sum_replay", "kls_status_string", "kls_last_error"]
 
 
@@ -89,6 +90,8 @@ def lib():
         L.kls_check.argtypes = [P]
         L.kls_debug_set_layout.argtypes = [P, C.POINTER(KlsDebugLayout)]
         L.kls_debug_time_verify.argtypes = [P, C.c_int, C.c_int, C.c_void_p, C.POINTER(C.c_double)]
+        L.kls_debug_run_verify_steps.argtypes = [P, C.c_void_p, C.c_int, C.c_int, I32P, C.POINTER(C.c_double), I32P,
+                                                 I32P, C.POINTER(C.c_int64), C.c_void_p]
         L.kls_debug_path.argtypes = [P, C.POINTER(C.c_int32)]
         L.kls_debug_expf.argtypes = [C.c_uint32, C.c_longlong, C.c_void_p, C.c_void_p]
         L.kls_debug_sum_replay.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_int, C.c_double, C.c_void_p,

@@ -886,6 +886,23 @@ int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, doub
     return check_fault(h);
 }
 
+int kls_debug_run_verify_steps(kls_handle h, const float* logits, int nb, int n_steps, const int32_t* drafts,
+                               const double* u, int32_t* out_tokens, int32_t* out_accepted, int64_t* out_step_ns,
+                               kls_stream stream) {
+    if (int st = check_handle(h)) return st;
+    if (n_steps < 1 || nb < 1 || !drafts || !u || !out_tokens || !out_accepted)
+        return fail(KLS_ERR_INVALID_ARG, "bad arguments");
+    for (int i = 0; i < n_steps; ++i) {
+        const auto t0 = std::chrono::steady_clock::now();
+        const int st = kls_verify(h, logits, nb, drafts + (int64_t) i * (nb > 1 ? nb - 1 : 0), u + (int64_t) i * nb,
+                                  out_tokens + (int64_t) i * nb, out_accepted + i, stream);
+        const auto t1 = std::chrono::steady_clock::now();
+        if (out_step_ns) out_step_ns[i] = std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+        if (st) return st;
+    }
+    return KLS_OK;
+}
+
 int kls_debug_path(kls_handle h, int32_t* out_path) {
     if (int st = check_handle(h)) return st;
     if (!out_path) return fail(KLS_ERR_INVALID_ARG, "null argument");
