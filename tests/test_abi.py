@@ -64,6 +64,8 @@ def test_null_handle_errors():
     assert L.kls_sample_batch(None, None, 1, 10, None, None, None, None, None) == _lib.KLS_ERR_INVALID_ARG
     assert L.kls_get_candidates(None, 0, None, None, 0, None, None) == _lib.KLS_ERR_INVALID_ARG
     assert L.kls_debug_expf(0, 10, None, None) == _lib.KLS_ERR_INVALID_ARG
+    assert L.kls_debug_run_verify_steps(None, None, 4, 1, None, None, None, None, None, None) == \
+        _lib.KLS_ERR_INVALID_ARG
 
 
 def test_no_device_is_reported_without_gpu():
