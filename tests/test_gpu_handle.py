@@ -83,6 +83,42 @@ def test_device_accept_prefix_and_results(torch_cuda, K, oracle_lib):
         S.close()
 
 
+def test_step_loop_hook(torch_cuda, K, oracle_lib):
+    """kls_debug_run_verify_steps (bench.py's timed loop): 12 verify steps with penalties run back to back from C,
+    each step's history the tokens the earlier ones accepted; tokens and accepted counts against the oracle's chain
+    of steps, and a wall time for every step."""
+    torch, O = torch_cuda, oracle_lib
+    rng = np.random.default_rng(21)
+    p = W.Params(temperature=0.7, top_k=20, top_p=0.95, presence_penalty=0.4, frequency_penalty=0.1,
+                 repetition_penalty=1.05, seed=9)
+    nb, n = 4, 12
+    x, _ = W._head_rows(rng, nb, V)
+    d = dev(torch, x)
+    counts = np.zeros(V, np.int32)
+    drafts = np.zeros((n, nb - 1), np.int32)
+    us = rng.random((n, nb))
+    exp = []
+    for i in range(n):
+        drafts[i] = oracle_drafts(O, x, p, us[i], counts, i % nb, rng)
+        ot, oa, counts = O.verify(x, drafts[i], p, us[i], counts, O.MODE_TOTAL)
+        exp.append((oa, list(ot[:oa + 1])))
+    S = K.Sampler(p, n_vocab=V)
+    toks = np.zeros((n, nb), np.int32)
+    acc = np.zeros(n, np.int32)
+    ns = np.zeros(n, np.int64)
+    I32P, F64P = C.POINTER(C.c_int32), C.POINTER(C.c_double)
+    say("step loop", n)
+    _lib.check(_lib.lib().kls_debug_run_verify_steps(
+        S._h, C.c_void_p(d.data_ptr()), nb, n, np.ascontiguousarray(drafts).ctypes.data_as(I32P),
+        np.ascontiguousarray(us).ctypes.data_as(F64P), toks.ctypes.data_as(I32P), acc.ctypes.data_as(I32P),
+        ns.ctypes.data_as(C.POINTER(C.c_int64)), None), "kls_debug_run_verify_steps")
+    for i in range(n):
+        oa, ot = exp[i]
+        assert acc[i] == oa and list(toks[i][:oa + 1]) == ot, i
+        assert ns[i] > 0
+    S.close()
+
+
 def test_graph_recaptured_when_counts_widen(torch_cuda, K, oracle_lib):
     """A verify graph captured while the history's counts fit 16 bits must not be replayed once an id's count
     can reach 65536: the step after the widening upload matches the oracle (a stale 16-bit table would wrap the
