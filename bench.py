@@ -203,8 +203,9 @@ def next_rows(torch, klein_amd, W):
 
 def topk_above_64(torch, klein_amd, W):
     """Top-k above 64 (src/sampler.cpp:42-51 with larger k), which no headline config uses: the verify step's
-    workload with k = 256 and 1,024 on the mid path (one kernel, captured in the step's graph), the 64-row batch
-    at k = 256, and a row without a limit on the wide path (keys, a device-wide sort, the tail: several launches).
+    workload with k = 256 and 1,024 on the mid path (one kernel, captured in the step's graph) and without a limit
+    on the wide path (keys, a device-wide sort, the tail: several kernels, captured in the step's graph), the
+    64-row batch at k = 256, and one row without a limit launched directly.
     Every timed call is checked against its first (untimed) result."""
     import numpy as np
     from klein_amd import _lib
@@ -216,9 +217,10 @@ def topk_above_64(torch, klein_amd, W):
     drafts = np.ascontiguousarray(v.drafts, dtype=np.int32)
     u = np.ascontiguousarray(v.u, dtype=np.float64)
     res = {}
-    for k in (256, 1024):
+    for k in (256, 1024, 0):
+        path = "mid" if k else "wide"
         S = klein_amd.Sampler(W.Params(temperature=0.6, top_k=k, top_p=0.95), n_vocab=V, max_rows=4)
-        assert S.path == "mid"
+        assert S.path == path
         h, sp = S._h, None
         t0, a0 = np.zeros(4, np.int32), C.c_int32()
         _lib.check(L.kls_verify(h, dptr, 4, drafts.ctypes.data_as(I32P), u.ctypes.data_as(F64P),
@@ -232,11 +234,12 @@ def topk_above_64(torch, klein_amd, W):
             lat.append((time.perf_counter_ns() - x0) / 1e3)
             if st:
                 _lib.check(st, "kls_verify")
-            assert ac.value == a0.value and list(tk[:ac.value + 1]) == list(t0[:a0.value + 1]), "mid verify step"
+            assert ac.value == a0.value and list(tk[:ac.value + 1]) == list(t0[:a0.value + 1]), f"{path} verify step"
         kus = C.c_double()
         _lib.check(L.kls_debug_time_verify(h, 50, 5, sp, C.byref(kus)), "kls_debug_time_verify")
-        res[f"verify_step_k{k}"] = {"path": "mid", "median_us": round(pct(lat, 50), 2),
-                                    "p99_us": round(pct(lat, 99), 2), "kernel_us": round(kus.value, 2)}
+        res[f"verify_step_k{k}" if k else "verify_step_no_limit"] = {
+            "path": path, "median_us": round(pct(lat, 50), 2), "p99_us": round(pct(lat, 99), 2),
+            "kernel_us": round(kus.value, 2)}
         S.close()
     # 64 rows at k = 256, no penalties
     wb = W.batched()
