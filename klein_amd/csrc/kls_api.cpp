@@ -536,12 +536,10 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
     if (max_rows < 1) return fail(KLS_ERR_INVALID_ARG, "max_rows must be positive");
     const int k = (params->top_k > 0 && params->top_k < n_vocab) ? params->top_k : n_vocab;
     // k above KCAP: the mid path up to MID_KMAX (while the rows' buffers hold every segment's share), else the
-    // wide path, whose keys hold an id and a row index in 32 bits
+    // wide path, whose radix sort indexes the rows' keys with 32 bits
     const bool mid = params->temperature > 0.0f && mid_fits(n_vocab, k);
     const bool wide = params->temperature > 0.0f && k > KCAP && !mid;
-    int row_bits = 0;
-    while ((1ll << row_bits) < (long long) max_rows) ++row_bits;
-    if (wide && wide_id_bits(n_vocab) + row_bits > 32)
+    if (wide && (long long) n_vocab * max_rows >= (1ll << 32))
         return fail(KLS_ERR_UNSUPPORTED, "top-k above 64 with this many rows of this vocabulary");
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
@@ -605,7 +603,7 @@ int kls_create(const kls_params* params, int n_vocab, int max_rows, kls_handle* 
         h->w.id_bits = wide_id_bits(n_vocab);
         ALLOC(h->w.keys, sizeof(uint64_t) * R * n_vocab);
         ALLOC(h->w.sorted, sizeof(uint64_t) * R * n_vocab);
-        ALLOC(h->w.counts, sizeof(uint32_t) * 256 * sort_tiles(R * (size_t) n_vocab));
+        ALLOC(h->w.counts, sizeof(uint32_t) * 256 * R * sort_tiles((size_t) n_vocab));
         h->w.chunks = (k + WT_CHUNK - 1) / WT_CHUNK;
         h->w.seg_cap = WT_SEGS;
         ALLOC(h->w.part, sizeof(double) * R * h->w.chunks);

@@ -122,10 +122,10 @@ constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 20;
 
 
 // Wide top-k (k above KCAP, up to no limit; src/sampler.cpp:42-51): every logit of a row becomes one 64-bit key
-//   (row field << (32 + id_bits)) | (order-preserving image of the (penalized) value << id_bits) | (~id & id mask)
-// with row field = n_rows - 1 - row, so one descending device-wide sort of all rows' keys leaves each row's keys
-// contiguous, value-descending and, on equal values, id-ascending (the fast path's order). NaN maps to the
-// value image 0, after every number. The sorted keys then go through the O(k) tail in reference order.
+//   (order-preserving image of the (penalized) value << id_bits) | (~id & id mask)
+// in id order, and a stable descending sort of each row on the value field leaves the row's keys
+// value-descending and, on equal values, id-ascending (the fast path's order). NaN maps to the value image 0,
+// after every number. The sorted keys then go through the O(k) tail in reference order.
 // The wide path's tail cuts each of its double chains into chunks of WT_CHUNK terms (kls_kernels.hip), and each
 // chunk into at most WT_SEGS segments, recorded in order:
 constexpr int WT_CHUNK = 2048, WT_SEGS = 64;
@@ -239,12 +239,13 @@ int wide_id_bits(int V);  // key bits the ids of a V-entry vocabulary take
 hipError_t launch_mid(const RowsArgs& a, const MidArgs& m, bool penalize, hipStream_t s);
 hipError_t prepare_mid_kernels();  // once per device: LDS limit of the kernel with a count table
 
-// Descending device-wide sort of n 64-bit keys (n < 2^32) on bits [begin_bit, end_bit) (kls_sort.hip): a stable
-// radix sort, 8 bits per pass, alternating between the buffers a (the input) and b; *result is the one that holds
-// the sorted keys. Keys equal on those bits keep their input order. counts: 256 * sort_tiles(n) words of scratch.
+// Descending sort of each of `rows` rows of row_len 64-bit keys (rows * row_len < 2^32; row r at r * row_len) on
+// bits [begin_bit, end_bit) (kls_sort.hip): a stable radix sort, 8 bits per pass, alternating between the buffers
+// a (the input) and b; *result is the one that holds the sorted keys. Keys equal on those bits keep their input
+// order. counts: 256 * rows * sort_tiles(row_len) words of scratch.
 constexpr int SORT_TILE = 8192;
 inline size_t sort_tiles(size_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
-hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int begin_bit, int end_bit, uint32_t* counts,
-                          uint64_t** result, hipStream_t s);
+hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
+                          uint32_t* counts, uint64_t** result, hipStream_t s);
 
 }  // namespace kls

@@ -1477,7 +1477,7 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
         __syncthreads();
     }
     const int ib = w.id_bits;
-    const uint64_t rf = (uint64_t) (a.n_rows - 1 - row) << (32 + ib);
+
     const uint32_t idm = (1u << ib) - 1u;
     uint64_t* __restrict__ out = w.keys + (int64_t) row * a.V;
     for (int id = lo + (int) threadIdx.x; id < hi; id += WIDE_WG) {
@@ -1486,7 +1486,7 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
             const uint32_t c = s_cnt[id - lo];
             if (c != 0u) x = penalize(x, c, a.p);
         }
-        out[id] = rf | ((uint64_t) ord_f32(x) << ib) | (uint64_t) (~(uint32_t) id & idm);
+        out[id] = ((uint64_t) ord_f32(x) << ib) | (uint64_t) (~(uint32_t) id & idm);
     }
 }
 
@@ -2841,13 +2841,11 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
         hipLaunchKernelGGL(wide_keys_kernel<false>, grid, dim3(WIDE_WG), 0, s, a, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    int rb = 0;
-    while ((1 << rb) < a.n_rows) ++rb;
-    const size_t n = (size_t) a.n_rows * a.V;
     uint64_t* sorted = nullptr;
-    // The keys are written in (row, id) order and the sort is stable, so sorting on the row and value fields
-    // alone leaves equal values in ascending id order, as the id field would: its passes are skipped.
-    e = sort_keys_desc(w.keys, w.sorted, n, w.id_bits, 32 + w.id_bits + rb, w.counts, &sorted, s);
+    // Each row's keys are sorted on their own. They are written in id order and the sort is stable, so sorting on
+    // the value field alone leaves equal values in ascending id order, as the id field would: its passes are
+    // skipped (4 passes of 8 bits).
+    e = sort_keys_desc(w.keys, w.sorted, a.n_rows, (size_t) a.V, w.id_bits, 32 + w.id_bits, w.counts, &sorted, s);
     if (e != hipSuccess) return e;
     // the tail reads the sorted buffer and keeps its terms in the other one: the three chains, each mapped per
     // chunk and resolved per row

@@ -1,10 +1,12 @@
-// Device-wide descending sort of 64-bit keys for the wide top-k path: a stable least-significant-digit radix sort,
-// 8 bits per pass, two kernels per pass (no memset, so a pass can be captured in a graph):
-//   1. sort_hist_kernel: each tile of SORT_TILE keys counts its digits in LDS, written tile-major:
-//      counts[tile * 256 + digit];
-//   2. sort_scatter_kernel: each tile finds where its keys of each digit start (the keys of smaller digits in all
-//      tiles, then those of its digit in earlier tiles: sums over the count table, read coalesced by four groups
-//      of 256 threads, and a scan over the 256 digit totals in LDS), ranks its keys stably and writes them there.
+// Descending sort of the rows of 64-bit keys for the wide top-k path, each row on its own: a stable
+// least-significant-digit radix sort, 8 bits per pass, two kernels per pass (no memset, so a pass can be captured
+// in a graph). Every row is cut into tiles of SORT_TILE keys (the last one partial); tile t of row r is
+// workgroup r * tiles_per_row + t.
+//   1. sort_hist_kernel: each tile counts its digits in LDS, written tile-major: counts[tile * 256 + digit];
+//   2. sort_scatter_kernel: each tile finds where its keys of each digit start in its row (the row's keys of
+//      smaller digits, then those of its digit in the row's earlier tiles: sums over the row's part of the count
+//      table, read coalesced by four groups of 256 threads, and a scan over the 256 digit totals in LDS), ranks
+//      its keys stably and writes them there.
 // Descending order is ascending order of the inverted digit (255 - digit). Within a tile, key i of the tile is
 // held by wave i / 512, slot (i / 64) % 8, lane i % 64; a wave ranks its 512 keys slot by slot: the lanes of a
 // slot whose digits are equal are found with eight ballots, a key's rank is the wave's count of that digit so far
@@ -23,21 +25,22 @@ __device__ __forceinline__ uint32_t rdigit(uint64_t k, int shift) { return 255u 
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
-// Index of key s of this thread in its tile (wave-major: each wave holds 512 consecutive keys).
-__device__ __forceinline__ size_t tile_index(unsigned tile, int wave, int s, int lane) {
-    return (size_t) tile * SORT_TILE + (size_t) wave * 512 + (size_t) s * 64 + lane;
-}
+// Offset of key s of this thread in its tile (wave-major: each wave holds 512 consecutive keys).
+__device__ __forceinline__ int tile_offset(int wave, int s, int lane) { return wave * 512 + s * 64 + lane; }
 
-__global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __restrict__ in, uint32_t n, int shift,
-                                                          uint32_t* __restrict__ counts) {
+__global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __restrict__ in, uint32_t row_len,
+                                                          uint32_t tpr, int shift, uint32_t* __restrict__ counts) {
     __shared__ uint32_t h[256];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t row = blockIdx.x / tpr, t = blockIdx.x - row * tpr;
+    const int lim = (int) min((uint32_t) SORT_TILE, row_len - t * SORT_TILE);  // keys in this tile
+    const uint64_t* __restrict__ src = in + (size_t) row * row_len + (size_t) t * SORT_TILE;
     if (tid < 256) h[tid] = 0u;
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
-        const size_t i = tile_index(blockIdx.x, wave, s, lane);
-        if (i < n) atomicAdd(&h[rdigit(in[i], shift)], 1u);
+        const int i = tile_offset(wave, s, lane);
+        if (i < lim) atomicAdd(&h[rdigit(src[i], shift)], 1u);
     }
     __syncthreads();
     if (tid < 256) counts[(size_t) blockIdx.x * 256 + tid] = h[tid];
@@ -46,31 +49,35 @@ __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __rest
 constexpr int SC_UNROLL = 8;  // count-table rows in flight per thread
 
 __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
-                                                             uint32_t n, int shift, uint32_t tiles,
+                                                             uint32_t row_len, uint32_t tpr, int shift,
                                                              const uint32_t* __restrict__ counts) {
     __shared__ uint32_t cw[ST_NW][256];  // per wave: digit counts so far, then the earlier waves' counts
     __shared__ uint32_t tb[256];         // this tile's first slot per digit
     __shared__ uint32_t part[2][4][256];  // the count sums of the four groups: earlier tiles, all tiles
     __shared__ uint32_t wsum[4];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t tile = blockIdx.x;
+    const uint32_t row = blockIdx.x / tpr, tile = blockIdx.x - row * tpr;  // (tile within the row)
+    const int lim = (int) min((uint32_t) SORT_TILE, row_len - tile * SORT_TILE);
+    const uint64_t* __restrict__ src = in + (size_t) row * row_len + (size_t) tile * SORT_TILE;
+    uint64_t* __restrict__ dst = out + (size_t) row * row_len;
+    const uint32_t* __restrict__ rc = counts + (size_t) row * tpr * 256;  // the row's part of the count table
     uint64_t k[ST_PER];
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
-        const size_t i = tile_index(tile, wave, s, lane);
-        k[s] = i < n ? in[i] : 0ull;
+        const int i = tile_offset(wave, s, lane);
+        k[s] = i < lim ? src[i] : 0ull;
     }
     for (int i = tid; i < ST_NW * 256; i += ST_WG) (&cw[0][0])[i] = 0u;
     {
-        // group g sums rows g, g + 4, ... of the count table for digit d
+        // group g sums the row's tiles g, g + 4, ... of the count table for digit d
         const int g = tid >> 8, d = tid & 255;
         uint32_t before = 0u, all = 0u;
-        for (uint32_t t0 = (uint32_t) g; t0 < tiles; t0 += 4 * SC_UNROLL) {
+        for (uint32_t t0 = (uint32_t) g; t0 < tpr; t0 += 4 * SC_UNROLL) {
             uint32_t v[SC_UNROLL];
 #pragma unroll
             for (int u = 0; u < SC_UNROLL; ++u) {
                 const uint32_t t = t0 + 4u * u;
-                v[u] = t < tiles ? counts[(size_t) t * 256 + d] : 0u;
+                v[u] = t < tpr ? rc[(size_t) t * 256 + d] : 0u;
             }
 #pragma unroll
             for (int u = 0; u < SC_UNROLL; ++u) {
@@ -106,7 +113,7 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     uint32_t rk[ST_PER];
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
-        const bool valid = tile_index(tile, wave, s, lane) < n;
+        const bool valid = tile_offset(wave, s, lane) < lim;
         const uint32_t d = rdigit(k[s], shift);
         uint64_t same = ballot64(valid);  // (all lanes take part in every ballot)
 #pragma unroll
@@ -133,26 +140,28 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
-        if (tile_index(tile, wave, s, lane) < n) {
+        if (tile_offset(wave, s, lane) < lim) {
             const uint32_t d = rdigit(k[s], shift);
             const uint32_t pos = tb[d] + cw[wave][d] + rk[s];
-            if (pos < n) out[pos] = k[s];  // (always: the counts are the tile's own)
+            if (pos < row_len) dst[pos] = k[s];  // (always: the counts are the row's own)
         }
     }
 }
 
 }  // namespace
 
-hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, size_t n, int begin_bit, int end_bit, uint32_t* counts,
-                          uint64_t** result, hipStream_t s) {
-    if (n == 0 || n >= (1ull << 32) || begin_bit < 0 || end_bit <= begin_bit || end_bit > 64)
+hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
+                          uint32_t* counts, uint64_t** result, hipStream_t s) {
+    if (rows < 1 || row_len == 0 || (size_t) rows * row_len >= (1ull << 32) || begin_bit < 0 ||
+        end_bit <= begin_bit || end_bit > 64)
         return hipErrorInvalidValue;
-    const uint32_t tiles = (uint32_t) sort_tiles(n);
+    const uint32_t tpr = (uint32_t) sort_tiles(row_len);
+    const dim3 grid((unsigned) rows * tpr);
     uint64_t* src = a;
     uint64_t* dst = b;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
-        hipLaunchKernelGGL(sort_hist_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, (uint32_t) n, shift, counts);
-        hipLaunchKernelGGL(sort_scatter_kernel, dim3(tiles), dim3(ST_WG), 0, s, src, dst, (uint32_t) n, shift, tiles,
+        hipLaunchKernelGGL(sort_hist_kernel, grid, dim3(ST_WG), 0, s, src, (uint32_t) row_len, tpr, shift, counts);
+        hipLaunchKernelGGL(sort_scatter_kernel, grid, dim3(ST_WG), 0, s, src, dst, (uint32_t) row_len, tpr, shift,
                            counts);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
