@@ -91,3 +91,44 @@ def test_random_sweep(torch_cuda, K, oracle_lib, block):
                 assert gkept == kept, (label, r, gkept, kept)
         S.check()
         S.close()
+
+
+@pytest.mark.parametrize("block", range(3))
+def test_random_verify_sweep(torch_cuda, K, oracle_lib, block):
+    """Verify steps (src/engine.cpp:563-575) over the handle's own history on every path: random nb, top-k,
+    temperature, top-p, min-p and penalties; the first m drafts are the oracle's own tokens on the accepted path
+    (so 0..nb-1 drafts are accepted); each step's tokens and accepted count against the oracle's chain."""
+    torch, O = torch_cuda, oracle_lib
+    rng = np.random.default_rng(3300 + block)
+    for case in range(8):
+        V = int(rng.choice([5000, 70001, 248320]))
+        nb = int(rng.choice([1, 2, 4, 8]))
+        k = int(rng.choice([1, 20, 64, 65, 300, 1024, 2000, 0]))
+        T = float(rng.choice([0.0, 0.6, 1.0, 1.8]))
+        tp = float(rng.choice([1.0, 0.95, 0.6]))
+        mp = float(rng.choice([0.0, 0.05]))
+        pen = int(rng.integers(3))
+        p = W.Params(temperature=T, top_k=k, top_p=tp, min_p=mp, seed=int(rng.integers(1, 1000)), **PENS[pen])
+        label = f"block {block} case {case}: V {V} nb {nb} k {k} T {T} top_p {tp} min_p {mp} pen {pen}"
+        print("[case]", label, flush=True)
+        x = make_rows(rng, str(rng.choice(["normal", "heads", "bf16"])), nb, V)
+        d = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+        S = K.Sampler(p, n_vocab=V, max_rows=max(nb, 1))
+        counts = np.zeros(V, np.int32)
+        for t in rng.integers(0, V, int(rng.integers(0, 300))):
+            S.accept(int(t))
+            counts[t] += 1
+        for step in range(3):
+            u = rng.random(nb)
+            m = int(rng.integers(0, nb))
+            drafts = rng.integers(0, V, max(nb - 1, 1)).astype(np.int32)
+            c = counts.copy()
+            for i in range(min(m, nb - 1)):
+                drafts[i] = O.sample(x[i], p, u[i], c if pen else None, O.MODE_TOTAL)[0]
+                c[drafts[i]] += 1
+            toks, acc = S.verify(d, drafts if nb > 1 else np.zeros(1, np.int32), u=u)
+            ot, oa, counts = O.verify(x, drafts[:nb - 1] if nb > 1 else np.zeros(0, np.int32), p, u, counts,
+                                      O.MODE_TOTAL)
+            assert acc == oa and list(toks) == list(ot[:oa + 1]), (label, step, acc, oa)
+        S.check()
+        S.close()
