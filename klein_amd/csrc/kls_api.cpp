@@ -56,9 +56,12 @@ int set_error(int status, const char* what, hipError_t e) { return fail(status, 
 // 64-row batch). Greedy rows merge trivially and read faster from more workgroups, so they skip this choice.
 // Otherwise short segments (256 threads x {4, 8, 16, 32} logits): the smallest length whose grid
 // (rows x segments) stays within target_wg workgroups (128: half the CUs; every segment of a row then takes the
-// row's ticket, and more segments wait longer on it than their shorter reads save). When even 8192 ids leave
+// row's ticket, and more segments wait longer on it than their shorter reads save), and for greedy rows at most
+// kGreedySegs segments per row (one wave then merges the row's maxima without a barrier: the one-row draft
+// argmax measured 3.5 us with 31 segments of 8192 ids, 3.6 with 61 of 4096, 4.4 with 122 of 2048). When even 8192 ids leave
 // too many workgroups, 1024-thread workgroups over 16384..65536 ids (one per CU), the smallest length within
 // wide_target_wg: every logit and the row's history are then read once per segment with the chip full.
+constexpr int kGreedySegs = 32;  // at most this many segments per greedy row on the short-segment layouts
 void choose_segments(int V, int rows, bool greedy, int seg_override, int target_wg, int wide_target_wg, int* seg_len,
                      int* segs) {
     auto grid = [&](int sl) { return (long long) rows * ((V + sl - 1) / sl); };
@@ -72,7 +75,7 @@ void choose_segments(int V, int rows, bool greedy, int seg_override, int target_
     } else if (few) {
         sl = few;
     } else {
-        while (sl < SEG_WIDE / 2 && grid(sl) > target_wg) sl *= 2;
+        while (sl < SEG_WIDE / 2 && (grid(sl) > target_wg || (greedy && (V + sl - 1) / sl > kGreedySegs))) sl *= 2;
         if (grid(sl) > target_wg) {
             sl = SEG_WIDE;
             while (sl < SEG_MAX && grid(sl) > wide_target_wg) sl *= 2;
