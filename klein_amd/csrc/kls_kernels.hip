@@ -1627,22 +1627,27 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
         const double A0 = ldexp(acc, 52 - E);  // (an integer in [2^52, 2^53))
         const uint32_t pi0 = dparity(A0);
         const int j0 = i + tid * RP_PT;
+        // a wave past the block's terms (uniform in the wave) loads, maps and walks nothing: it holds
+        // identities and takes the barriers and the block's total with the others
+        const bool live = i + wave * 64 * RP_PT < n;
         double tv[RP_PT];  // this thread's terms (addresses clamped to the chain; terms past it are not used)
-#pragma unroll
-        for (int q = 0; q < RP_PT; ++q) tv[q] = NEG ? -t[min(j0 + q, n - 1)] : t[min(j0 + q, n - 1)];
-        // the composed map of this thread's terms
         ParMap M = par_identity();
+        if (live) {
 #pragma unroll
-        for (int q = 0; q < RP_PT; ++q) {
-            double f;
-            bool c;
-            const ParMap m = term_map(tv[q], E, &f, &c);
-            if (j0 + q < n) M = par_compose(M, m);
+            for (int q = 0; q < RP_PT; ++q) tv[q] = NEG ? -t[min(j0 + q, n - 1)] : t[min(j0 + q, n - 1)];
+            // the composed map of this thread's terms
+#pragma unroll
+            for (int q = 0; q < RP_PT; ++q) {
+                double f;
+                bool c;
+                const ParMap m = term_map(tv[q], E, &f, &c);
+                if (j0 + q < n) M = par_compose(M, m);
+            }
         }
-        // workgroup scan of the threads' maps: each wave's (DPP; a wave past the terms holds identities and
-        // skips it), then the waves' totals (a 16-lane DPP scan that every wave runs on the totals it reads back)
+        // workgroup scan of the threads' maps: each wave's (DPP), then the waves' totals (a 16-lane DPP scan
+        // that every wave runs on the totals it reads back)
         ParMap x = par_identity(), xe = par_identity();
-        if (i + wave * 64 * RP_PT < n) {  // (uniform in the wave)
+        if (live) {
             x = wave_scan_map<false>(M);
             xe = dpp_map<0x138, 0xf>(x);  // wave_shr:1: the maps before this lane (lane 0: identity)
         }
@@ -1660,7 +1665,7 @@ __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F 
 #pragma unroll
         for (int q = 0; q < RP_PT; ++q) {
             const int j = j0 + q;
-            if (hq < 0 && j < n) {
+            if (live && hq < 0 && j < n) {
                 const double tj = tv[q];
                 double f;
                 bool cross;
@@ -1767,18 +1772,24 @@ __device__ __forceinline__ bool sums_exact(double mn, double tot) {
 // (t[i] <- cum_i); the draw. Returns the drawn candidate with *n_kept and this thread's p_i, or -1 (t untouched)
 // when a chain is not exact in every order and must be replayed. The exactness of the cumulative chain is
 // judged over all kk terms, which covers the kept prefix.
+// Waves past the candidates (wave * 64 >= kk) only post neutral values (sum 0, least term +inf, no index) and
+// take the barriers and the workgroup-wide decisions with the others; the caller uses the result on wave 0.
 __device__ int tail_exact(double* t, int kk, const SamplingParams& p, double u, int lane, int wave, int* n_kept,
                           float* p_mine) {
     const int tid = (int) threadIdx.x;
     const bool in = tid < kk;
-    const double e = in ? t[tid] : 0.0;
-    const double e0 = t[0];
-    {
+    const bool live = wave * 64 < kk;  // (uniform in the wave)
+    double e = 0.0;
+    if (live) {
+        e = in ? t[tid] : 0.0;
         const double sw = wave_sum_f64(e, lane), mw = wave_min_pos(e, lane);
         if (lane == 0) {
             s_tx_sum[wave] = sw;
             s_tx_min[wave] = mw;
         }
+    } else if (lane == 0) {
+        s_tx_sum[wave] = 0.0;
+        s_tx_min[wave] = (double) INFINITY;
     }
     __syncthreads();
     double sum = 0.0, mn = (double) INFINITY;
@@ -1789,18 +1800,24 @@ __device__ int tail_exact(double* t, int kk, const SamplingParams& p, double u, 
     }
     if (!sums_exact(mn, sum)) return -1;
     // p_i (:60) and min-p (:62-68): the first i >= 1 with p_i < p_0 * min_p ends the list
-    const float pf = in ? __double2float_rn(__ddiv_rn(e, sum)) : 0.0f;
-    const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(e0, sum)), p.min_p);
-    const uint64_t bm = ballot(p.min_p > 0.0f && in && tid >= 1 && !(pf >= thr));
-    const double x = in ? (double) pf : 0.0;
-    const double cw = wave_scan_f64(x);
-    {
+    float pf = 0.0f;
+    double cw = 0.0;
+    if (live) {
+        pf = in ? __double2float_rn(__ddiv_rn(e, sum)) : 0.0f;
+        const float thr = __fmul_rn(__double2float_rn(__ddiv_rn(t[0], sum)), p.min_p);
+        const uint64_t bm = ballot(p.min_p > 0.0f && in && tid >= 1 && !(pf >= thr));
+        const double x = in ? (double) pf : 0.0;
+        cw = wave_scan_f64(x);
         const double tw = rdlaned(cw, 63), mw = wave_min_pos(x, lane);
         if (lane == 0) {
             s_tx_tot[wave] = tw;
             s_tx_pmin[wave] = mw;
             s_tx_mp[wave] = bm ? wave * 64 + __builtin_ctzll(bm) : 0x7fffffff;
         }
+    } else if (lane == 0) {
+        s_tx_tot[wave] = 0.0;
+        s_tx_pmin[wave] = (double) INFINITY;
+        s_tx_mp[wave] = 0x7fffffff;
     }
     __syncthreads();
     double before = 0.0, tot = 0.0, pmn = (double) INFINITY;
@@ -1816,9 +1833,13 @@ __device__ int tail_exact(double* t, int kk, const SamplingParams& p, double u, 
     if (!sums_exact(pmn, tot)) return -1;
     // top-p (:69-79): the first i with cum_i >= top_p keeps i + 1; the draw total (:80-81) is cum_{n-1}
     const double cum = before + cw;
-    if (in) t[tid] = cum;  // (every thread read e_0 before the barrier above)
-    const uint64_t bt = ballot(tid < n && cum >= (double) p.top_p);
-    if (lane == 0) s_tx_tp[wave] = bt ? wave * 64 + __builtin_ctzll(bt) : 0x7fffffff;
+    if (live) {
+        if (in) t[tid] = cum;  // (every thread read e_0 before the barrier above)
+        const uint64_t bt = ballot(tid < n && cum >= (double) p.top_p);
+        if (lane == 0) s_tx_tp[wave] = bt ? wave * 64 + __builtin_ctzll(bt) : 0x7fffffff;
+    } else if (lane == 0) {
+        s_tx_tp[wave] = 0x7fffffff;
+    }
     __syncthreads();
     if (p.top_p < 1.0f) {
         int f = 0x7fffffff;
@@ -1828,9 +1849,13 @@ __device__ int tail_exact(double* t, int kk, const SamplingParams& p, double u, 
     }
     // draw (:82-88): r = u*(total-0)+0; r - cum_i is exact while positive and keeps its sign at the step where it
     // reaches <= 0, so the drawn candidate is the first i with cum_i >= r (the last kept if none)
-    const double r0 = __dadd_rn(__dmul_rn(u, __dsub_rn(t[n - 1], 0.0)), 0.0);
-    const uint64_t bd = ballot(tid < n && cum >= r0);
-    if (lane == 0) s_tx_dr[wave] = bd ? wave * 64 + __builtin_ctzll(bd) : 0x7fffffff;
+    if (live) {
+        const double r0 = __dadd_rn(__dmul_rn(u, __dsub_rn(t[n - 1], 0.0)), 0.0);
+        const uint64_t bd = ballot(tid < n && cum >= r0);
+        if (lane == 0) s_tx_dr[wave] = bd ? wave * 64 + __builtin_ctzll(bd) : 0x7fffffff;
+    } else if (lane == 0) {
+        s_tx_dr[wave] = 0x7fffffff;
+    }
     __syncthreads();
     int f = 0x7fffffff;
 #pragma unroll
@@ -1883,7 +1908,7 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
     // e_i (:55-58) of every candidate, and kk: the first NaN key ends the candidates
     if (tid == 0) s_wide_n = k;
     __syncthreads();
-    {
+    if (wave * 64 < k) {  // (waves past the candidates have no term)
         const uint32_t o = fmt.img(K[min(tid, k - 1)]);
         const float e = expf_glibc_tab(__fdiv_rn(__fsub_rn(unord_f32(o), maxl), p.temperature), kExp2Tab[lane & 31]);
         if (tid < k) {
@@ -2711,6 +2736,12 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
     __syncthreads();
     const int N = min(s_mid_base, MID_ROWCAP);
     const int k = m.k;
+    // Key g of the buffer sits in register g / WG of thread g % WG (the loads issued together). Only the first
+    // RV registers hold keys; the loops over them end at the first group of four past RV (a scalar bound: the
+    // workgroup's one CU issues every instruction of all 16 waves, so registers that hold nothing would still
+    // cost issue slots, and a branch per register costs more than it saves).
+    const int RV = __builtin_amdgcn_readfirstlane((N + WG - 1) / WG);
+    static_assert(MID_RK % 4 == 0, "groups of four registers");
     uint64_t rk[MID_RK];
 #pragma unroll
     for (int r = 0; r < MID_RK; ++r) {
@@ -2720,7 +2751,10 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
     auto cnt2 = [&](uint64_t t) {
         int c = 0;
 #pragma unroll
-        for (int r = 0; r < MID_RK; ++r) c += rk[r] >= t ? 1 : 0;
+        for (int r = 0; r < MID_RK; ++r) {
+            if (r % 4 == 0 && r >= RV) break;
+            c += rk[r] >= t ? 1 : 0;
+        }
         return c;
     };
     uint64_t T2 = 1ull;  // (every buffered key: all are numbers)
@@ -2728,6 +2762,7 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
         uint32_t q1 = 0u, q2 = 0u;
 #pragma unroll
         for (int r = 0; r < MID_RK; ++r) {
+            if (r % 4 == 0 && r >= RV) break;
             const uint32_t ov = (uint32_t) (rk[r] >> 32);
             q2 = max(q2, min(q1, ov));
             q1 = max(q1, ov);
@@ -2751,6 +2786,7 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
     for (int i = n2 + tid; i < P; i += WG) S[i] = 0ull;
 #pragma unroll
     for (int r = 0; r < MID_RK; ++r) {
+        if (r % 4 == 0 && r >= RV) break;
         if (rk[r] >= T2) {
             if (o2 < MID_SORT) S[o2] = rk[r];
             ++o2;
