@@ -2553,24 +2553,27 @@ __device__ __forceinline__ uint64_t mid_narrow(const RowsArgs& a, F cnt, uint64_
     return ~0ull;
 }
 
-// Sorts S[0..P) descending with the workgroup (P a power of two in [64, MID_SORT]; U: LDS of the same size for
-// the exchanges). Element i lives in lane i % 64 of wave (i / 64) % 16, register i / 1024: strides below 64 are
-// bitonic steps across lanes, strides of 1024 and 2048 compare a thread's own registers, and strides 64..512 go
-// through LDS, the two buffers alternating so that each such step needs one barrier. Returns the buffer that
-// holds the result (after a barrier).
-__device__ __forceinline__ uint64_t* mid_sort(uint64_t* S, uint64_t* U, int P, int lane, int wave) {
+// Sorts S[0..P) descending with the workgroup, S = the first MID_SORT keys of the LDS words s_cnt (P a power of
+// two in [64, MID_SORT]; the next MID_SORT keys, U, serve the exchanges). Element i lives in lane i % 64 of wave
+// (i / 64) % 16, register i / 1024: strides below 64 are bitonic steps across lanes, strides of 1024 and 2048
+// compare a thread's own registers, and strides 64..512 go through LDS, the two halves alternating so that each
+// such step needs one barrier. Returns the offset in keys (0: S, MID_SORT: U) of the half that holds the result
+// (after a barrier). Every access indexes s_cnt itself, so it compiles to LDS instructions: a pointer chosen
+// between the halves at run time would be a generic address, and generic (FLAT) accesses to LDS take the
+// vector memory path (each exchange step then cost ~0.5 us more).
+__device__ __forceinline__ int mid_sort(int P, int lane, int wave) {
     constexpr int R = MID_SORT / MID_WG;
+    uint64_t* const L = reinterpret_cast<uint64_t*>(s_cnt);
     const int nch = P >> 6;  // chunks of 64
     uint64_t x[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int c = r * MID_NW + wave;
-        x[r] = c < nch ? S[c * 64 + lane] : 0ull;
+        x[r] = c < nch ? L[c * 64 + lane] : 0ull;
         // chunks alternately descending and ascending: every block of 128 is then bitonic
         if (c < nch) x[r] = (c & 1) ? sort64<false>(x[r], lane) : sort64<true>(x[r], lane);
     }
-    uint64_t* bufs[2] = {U, S};
-    int nb = 0;
+    int bo = MID_SORT;  // the half the next exchange writes (U first, then alternating)
     for (int size = 128; size <= P; size <<= 1) {
         for (int stride = size >> 1; stride >= 64; stride >>= 1) {
             if (stride >= MID_WG) {
@@ -2587,12 +2590,12 @@ __device__ __forceinline__ uint64_t* mid_sort(uint64_t* S, uint64_t* U, int P, i
                     }
                 }
             } else {
-                uint64_t* B = bufs[nb];
-                nb ^= 1;
+                const int b = bo;
+                bo ^= MID_SORT;
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const int c = r * MID_NW + wave;
-                    if (c < nch) B[c * 64 + lane] = x[r];
+                    if (c < nch) L[b + c * 64 + lane] = x[r];
                 }
                 __syncthreads();
 #pragma unroll
@@ -2600,7 +2603,7 @@ __device__ __forceinline__ uint64_t* mid_sort(uint64_t* S, uint64_t* U, int P, i
                     const int c = r * MID_NW + wave;
                     if (c < nch) {
                         const int i = c * 64 + lane;
-                        const uint64_t y = B[i ^ stride];
+                        const uint64_t y = L[b + (i ^ stride)];
                         const bool lower = (i & stride) == 0, desc = (i & size) == 0;
                         x[r] = (lower == desc) ? max64(x[r], y) : min64(x[r], y);
                     }
@@ -2613,14 +2616,13 @@ __device__ __forceinline__ uint64_t* mid_sort(uint64_t* S, uint64_t* U, int P, i
             if (c < nch) x[r] = ((c * 64) & size) == 0 ? bitonic_stage<64, true>(x[r], lane) : bitonic_stage<64, false>(x[r], lane);
         }
     }
-    uint64_t* out = bufs[nb];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int c = r * MID_NW + wave;
-        if (c < nch) out[c * 64 + lane] = x[r];
+        if (c < nch) L[bo + c * 64 + lane] = x[r];
     }
     __syncthreads();
-    return out;
+    return bo;
 }
 
 template <bool PENALIZE>
@@ -2780,7 +2782,6 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
     int o2 = mid_prefix(cnt2(T2), lane, wave, par, &n2);
     n2 = min(n2, MID_SORT);
     uint64_t* const S = reinterpret_cast<uint64_t*>(s_cnt);  // (the count table is no longer needed)
-    uint64_t* const U = S + MID_SORT;
     int P = 64;
     while (P < n2) P <<= 1;
     for (int i = n2 + tid; i < P; i += WG) S[i] = 0ull;
@@ -2793,8 +2794,8 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
         }
     }
     __syncthreads();
-    uint64_t* const K = mid_sort(S, U, P, lane, wave);
-    sorted_tail(a, row, K, min(k, n2), reinterpret_cast<double*>(K == S ? U : S), cin, FastKeyFmt{});
+    const int ko = mid_sort(P, lane, wave);
+    sorted_tail(a, row, S + ko, min(k, n2), reinterpret_cast<double*>(S + (MID_SORT - ko)), cin, FastKeyFmt{});
 }
 
 // LDS of the history count table: 4 bytes per id for 4-wave workgroups, 2 for 16-wave ones.
