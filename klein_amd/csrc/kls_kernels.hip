@@ -786,6 +786,32 @@ __device__ __forceinline__ double dpp_f64(double x) {
     return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);  // 0.0 where the source lane is outside the row
 }
 
+// Integer forms of wave_sum_f64 above and wave_scan_f64 below (every lane active): the wave's total in every
+// lane, and the inclusive prefix sum across the wave.
+__device__ __forceinline__ int wave_sum_i32(int x, int lane) {
+    x += xor_lane<32>(x, lane);
+    x += xor_lane<16>(x, lane);
+    x += xor_lane<8>(x, lane);
+    x += xor_lane<4>(x, lane);
+    x += xor_lane<2>(x, lane);
+    return x + xor_lane<1>(x, lane);
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_i32(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xf, false);  // 0 where the source lane is outside the row
+}
+
+__device__ __forceinline__ int wave_scan_i32(int x) {
+    x += dpp_i32<0x111, 0xf>(x);
+    x += dpp_i32<0x112, 0xf>(x);
+    x += dpp_i32<0x114, 0xf>(x);
+    x += dpp_i32<0x118, 0xf>(x);
+    x += dpp_i32<0x142, 0xa>(x);
+    x += dpp_i32<0x143, 0xc>(x);
+    return x;
+}
+
 // Inclusive prefix sum across the wave (row_shr within rows of 16, then row broadcasts of lanes 15 and 31).
 __device__ __forceinline__ double wave_scan_f64(double x) {
     x += dpp_f64<0x111, 0xf>(x);
@@ -2495,9 +2521,7 @@ __device__ __forceinline__ uint32_t wave_top2_kth(uint32_t m1, uint32_t m2, int 
 // Workgroup sum of c (every thread calls it). `par` alternates the LDS slots, so one barrier per call suffices:
 // a thread writes a slot again only after a later call's barrier, which every thread passes after its reads.
 __device__ __forceinline__ int mid_sum(int c, int lane, int wave, int& par) {
-    int x = c;
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
+    const int x = wave_sum_i32(c, lane);
     if (lane == 0) s_mid_c[par][wave] = x;
     __syncthreads();
     int tot = 0;
@@ -2509,12 +2533,7 @@ __device__ __forceinline__ int mid_sum(int c, int lane, int wave, int& par) {
 
 // Exclusive prefix of c over the workgroup's threads (thread order), and the total.
 __device__ __forceinline__ int mid_prefix(int c, int lane, int wave, int& par, int* total) {
-    int x = c;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x, d, 64);
-        x += lane >= d ? y : 0;
-    }
+    const int x = wave_scan_i32(c);
     if (lane == 63) s_mid_c[par][wave] = x;
     __syncthreads();
     int tot = 0, before = 0;
