@@ -85,6 +85,17 @@ void choose_segments(int V, int rows, bool greedy, int seg_override, int target_
     *segs = (V + sl - 1) / sl;
 }
 
+// Greedy rows in the checked (not whole-float4) form keep to 32,768-id segments: the 65,536-id form of that kernel
+// needs more than the 128 registers a 1024-thread workgroup allows and spills (64 rows of 248,319 ids, row stride
+// 248,320: 42.1 us against 23.8 us with penalties, 14.9 against 14.5 without). The sampling kernels' checked forms
+// keep 65,536 (22.7 us against 30.9).
+void fit_segments(bool greedy, const float* logits, int64_t stride, int V, int* seg_len, int* segs) {
+    if (greedy && *seg_len > 32768 && !rows_full(logits, stride, V, *seg_len)) {
+        *seg_len = 32768;
+        *segs = (V + 32767) / 32768;
+    }
+}
+
 SamplingParams sampling_params(const kls_params& p, int k) {
     return SamplingParams{p.temperature, p.top_p, p.min_p, p.presence_penalty, p.frequency_penalty,
                           p.repetition_penalty, std::min(k, KCAP), 1.0 / (double) p.repetition_penalty,
@@ -296,6 +307,7 @@ RowsArgs base_args(kls_sampler* h, const float* logits, int rows, int64_t stride
         a.segs = mid_segments(h->V);
     } else {
         segments_for(h, rows, greedy, &a.seg_len, &a.segs);
+        if (!h->seg_len_override) fit_segments(greedy, logits, stride, h->V, &a.seg_len, &a.segs);
     }
     a.p = h->sp;
     a.bucket_shift = h->bucket_shift;

@@ -211,6 +211,14 @@ struct PplArgs {
 // are the grid sizes the choice aims at (defaults 128 and 320).
 void choose_segments(int V, int rows, bool greedy, int seg_override, int target_wg, int wide_target_wg, int* seg_len,
                      int* segs);
+// The kernels' whole-float4 form: every row starts on a 16-byte boundary, the stride and V are multiples of 4 and no
+// segment is partial (V >= seg_len). Otherwise every float4 is checked against the segment's end.
+inline bool rows_full(const float* logits, int64_t stride, int V, int seg_len) {
+    return (stride & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (V & 3) == 0 && V >= seg_len;
+}
+// Greedy rows in the checked form (not rows_full) take at most 32,768-id segments: with 65,536 ids that kernel
+// runs out of registers and spills (kls_api.cpp).
+void fit_segments(bool greedy, const float* logits, int64_t stride, int V, int* seg_len, int* segs);
 constexpr int DEFAULT_TARGET_WG = 128, DEFAULT_WIDE_TARGET_WG = 320;
 // Grids of more (row, segment) workgroups than this share per-row running bounds through device memory.
 constexpr int DEFAULT_SHARE_MIN_WG = 1024;

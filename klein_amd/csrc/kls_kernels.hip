@@ -2846,10 +2846,8 @@ hipError_t launch_gpf(const RowsArgs& a, hipStream_t s) {
 
 template <bool G, bool P>
 hipError_t launch_gp(const RowsArgs& a, hipStream_t s) {
-    // whole aligned float4s everywhere: the row start and stride allow 16-byte loads and no segment is partial
-    const bool full = ((a.row_stride & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.logits) & 15u) == 0) &&
-                      (a.V & 3) == 0 && a.V >= a.seg_len;
-    return full ? launch_gpf<G, P, true>(a, s) : launch_gpf<G, P, false>(a, s);
+    return rows_full(a.logits, a.row_stride, a.V, a.seg_len) ? launch_gpf<G, P, true>(a, s)
+                                                               : launch_gpf<G, P, false>(a, s);
 }
 
 template <bool G, bool P, bool F, int NW, int EPT>

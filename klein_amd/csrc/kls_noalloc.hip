@@ -80,6 +80,8 @@ extern "C" int kls_sample_batch_noalloc(const kls_params* params, int n_vocab, c
     if (n_rows > NA_MAX_ROWS) return set_error(KLS_ERR_RANGE, "n_rows above KLS_NOALLOC_MAX_ROWS");
     int seg_len = 0, segs = 0;
     choose_segments(n_vocab, n_rows, greedy, 0, DEFAULT_TARGET_WG, DEFAULT_WIDE_TARGET_WG, &seg_len, &segs);
+    if ((long long) n_rows * ((n_vocab + 32767) / 32768) <= NA_MAX_ITEMS)
+        fit_segments(greedy, d_logits, row_stride, n_vocab, &seg_len, &segs);
     if ((long long) n_rows * segs > NA_MAX_ITEMS)
         return set_error(KLS_ERR_RANGE, "rows x segments above KLS_NOALLOC_MAX_WORKGROUPS");
     void* base = nullptr;
