@@ -6,7 +6,9 @@
 //   2. sort_scatter_kernel: each tile finds where its keys of each digit start in its row (the row's keys of
 //      smaller digits, then those of its digit in the row's earlier tiles: sums over the row's part of the count
 //      table, read coalesced by four groups of 256 threads, and a scan over the 256 digit totals in LDS), ranks
-//      its keys stably and writes them there.
+//      its keys stably, places them in digit order in LDS and writes them from there, so that neighbouring
+//      threads write neighbouring slots of each digit's run (written straight from the ranking, a wave's 64
+//      keys of random low digits went to up to 64 cache lines).
 // Descending order is ascending order of the inverted digit (255 - digit). Within a tile, key i of the tile is
 // held by wave i / 512, slot (i / 64) % 8, lane i % 64; a wave ranks its 512 keys slot by slot: the lanes of a
 // slot whose digits are equal are found with eight ballots, a key's rank is the wave's count of that digit so far
@@ -54,7 +56,9 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     __shared__ uint32_t cw[ST_NW][256];  // per wave: digit counts so far, then the earlier waves' counts
     __shared__ uint32_t tb[256];         // this tile's first slot per digit
     __shared__ uint32_t part[2][4][256];  // the count sums of the four groups: earlier tiles, all tiles
-    __shared__ uint32_t wsum[4];
+    __shared__ uint32_t wsum[4], wsum2[4];
+    __shared__ uint32_t ts[256];          // this tile's first slot per digit within the tile
+    __shared__ uint64_t sk[SORT_TILE];    // the tile's keys in digit order
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t row = blockIdx.x / tpr, tile = blockIdx.x - row * tpr;  // (tile within the row)
     const int lim = (int) min((uint32_t) SORT_TILE, row_len - tile * SORT_TILE);
@@ -128,7 +132,9 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
         if (valid && before == 0u) cw[wave][d] = prev + (uint32_t) __popcll(same);
     }
     __syncthreads();
+    uint32_t tile_before = 0u;
     if (tid < 256) {
+        // the earlier waves' counts per digit, and the tile's count of digit tid scanned over the digits
         uint32_t run = 0u;
 #pragma unroll
         for (int w = 0; w < ST_NW; ++w) {
@@ -136,14 +142,42 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
             cw[w][tid] = run;
             run += v;
         }
+        uint32_t x = run;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t y = (uint32_t) __shfl_up((int) x, (unsigned) d, 64);
+            x += lane >= d ? y : 0u;
+        }
+        if (lane == 63) wsum2[wave] = x;
+        tile_before = x - run;
     }
     __syncthreads();
+    if (tid < 256) {
+        uint32_t add = 0u;
+#pragma unroll
+        for (int w = 0; w < 3; ++w) add += w < wave ? wsum2[w] : 0u;
+        ts[tid] = tile_before + add;
+    }
+    __syncthreads();
+    // the tile's keys in digit order (stable: wave, then slot, then lane order within a digit)
 #pragma unroll
     for (int s = 0; s < ST_PER; ++s) {
         if (tile_offset(wave, s, lane) < lim) {
             const uint32_t d = rdigit(k[s], shift);
-            const uint32_t pos = tb[d] + cw[wave][d] + rk[s];
-            if (pos < row_len) dst[pos] = k[s];  // (always: the counts are the row's own)
+            sk[ts[d] + cw[wave][d] + rk[s]] = k[s];
+        }
+    }
+    __syncthreads();
+    // slot i of the tile goes to the row's slot of its digit: the digit's first row slot for this tile plus its
+    // place in the digit's run
+#pragma unroll
+    for (int s = 0; s < ST_PER; ++s) {
+        const int i = s * ST_WG + tid;
+        if (i < lim) {
+            const uint64_t key = sk[i];
+            const uint32_t d = rdigit(key, shift);
+            const uint32_t pos = tb[d] + (uint32_t) i - ts[d];
+            if (pos < row_len) dst[pos] = key;  // (always: the counts are the row's own)
         }
     }
 }
