@@ -250,9 +250,9 @@ hipError_t prepare_mid_kernels();  // once per device: LDS limit of the kernel w
 // Descending sort of each of `rows` rows of row_len 64-bit keys (rows * row_len < 2^32; row r at r * row_len) on
 // bits [begin_bit, end_bit) (kls_sort.hip): a stable radix sort, 8 bits per pass, alternating between the buffers
 // a (the input) and b; *result is the one that holds the sorted keys. Keys equal on those bits keep their input
-// order. counts: 256 * rows * sort_tiles(row_len) words of scratch.
-constexpr int SORT_TILE = 8192;
-inline size_t sort_tiles(size_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
+// order. counts: 256 * rows * sort_tiles(row_len) words of scratch (enough for every tile size the sort picks).
+constexpr int SORT_TILE_MIN = 2048;
+inline size_t sort_tiles(size_t n) { return (n + SORT_TILE_MIN - 1) / SORT_TILE_MIN; }
 hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
                           uint32_t* counts, uint64_t** result, hipStream_t s);
 

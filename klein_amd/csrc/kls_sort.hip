@@ -1,7 +1,7 @@
 // Descending sort of the rows of 64-bit keys for the wide top-k path, each row on its own: a stable
 // least-significant-digit radix sort, 8 bits per pass, two kernels per pass (no memset, so a pass can be captured
-// in a graph). Every row is cut into tiles of SORT_TILE keys (the last one partial); tile t of row r is
-// workgroup r * tiles_per_row + t.
+// in a graph). Every row is cut into tiles of 1024 * PER keys (PER = 2, 4 or 8 keys per thread, chosen per launch;
+// the last tile partial); tile t of row r is workgroup r * tiles_per_row + t.
 //   1. sort_hist_kernel: each tile counts its digits in LDS, written tile-major: counts[tile * 256 + digit];
 //   2. sort_scatter_kernel: each tile finds where its keys of each digit start in its row (the row's keys of
 //      smaller digits, then those of its digit in the row's earlier tiles: sums over the row's part of the count
@@ -10,7 +10,7 @@
 //      threads write neighbouring slots of each digit's run (written straight from the ranking, a wave's 64
 //      keys of random low digits went to up to 64 cache lines).
 // Descending order is ascending order of the inverted digit (255 - digit). Within a tile, key i of the tile is
-// held by wave i / 512, slot (i / 64) % 8, lane i % 64; a wave ranks its 512 keys slot by slot: the lanes of a
+// held by wave i / (64 PER), slot (i / 64) % PER, lane i % 64; a wave ranks its keys slot by slot: the lanes of a
 // slot whose digits are equal are found with eight ballots, a key's rank is the wave's count of that digit so far
 // plus the equal lanes below it, and the lowest of those lanes adds the group's size to the wave's count (the
 // wave's LDS operations run in order). Then an exclusive prefix over the waves per digit gives every key its
@@ -20,28 +20,31 @@
 namespace kls {
 namespace {
 
-constexpr int ST_WG = 1024, ST_NW = ST_WG / 64, ST_PER = SORT_TILE / ST_WG;
-static_assert(ST_PER * 64 * ST_NW == SORT_TILE && ST_PER == 8, "tile layout");
+constexpr int ST_WG = 1024, ST_NW = ST_WG / 64;
+static_assert(2 * ST_WG == SORT_TILE_MIN, "the smallest tile: two keys per thread");
 
 __device__ __forceinline__ uint32_t rdigit(uint64_t k, int shift) { return 255u - (uint32_t) ((k >> shift) & 255u); }
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
-// Offset of key s of this thread in its tile (wave-major: each wave holds 512 consecutive keys).
-__device__ __forceinline__ int tile_offset(int wave, int s, int lane) { return wave * 512 + s * 64 + lane; }
+// Offset of key s of this thread in its tile (wave-major: each wave holds 64 * PER consecutive keys).
+template <int PER>
+__device__ __forceinline__ int tile_offset(int wave, int s, int lane) { return wave * (PER * 64) + s * 64 + lane; }
 
+template <int PER>
 __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __restrict__ in, uint32_t row_len,
                                                           uint32_t tpr, int shift, uint32_t* __restrict__ counts) {
     __shared__ uint32_t h[256];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t row = blockIdx.x / tpr, t = blockIdx.x - row * tpr;
-    const int lim = (int) min((uint32_t) SORT_TILE, row_len - t * SORT_TILE);  // keys in this tile
-    const uint64_t* __restrict__ src = in + (size_t) row * row_len + (size_t) t * SORT_TILE;
+    constexpr int TILE = PER * ST_WG;
+    const int lim = (int) min((uint32_t) TILE, row_len - t * TILE);  // keys in this tile
+    const uint64_t* __restrict__ src = in + (size_t) row * row_len + (size_t) t * TILE;
     if (tid < 256) h[tid] = 0u;
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < ST_PER; ++s) {
-        const int i = tile_offset(wave, s, lane);
+    for (int s = 0; s < PER; ++s) {
+        const int i = tile_offset<PER>(wave, s, lane);
         if (i < lim) atomicAdd(&h[rdigit(src[i], shift)], 1u);
     }
     __syncthreads();
@@ -50,6 +53,7 @@ __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __rest
 
 constexpr int SC_UNROLL = 8;  // count-table rows in flight per thread
 
+template <int PER>
 __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
                                                              uint32_t row_len, uint32_t tpr, int shift,
                                                              const uint32_t* __restrict__ counts) {
@@ -58,17 +62,18 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     __shared__ uint32_t part[2][4][256];  // the count sums of the four groups: earlier tiles, all tiles
     __shared__ uint32_t wsum[4], wsum2[4];
     __shared__ uint32_t ts[256];          // this tile's first slot per digit within the tile
-    __shared__ uint64_t sk[SORT_TILE];    // the tile's keys in digit order
+    constexpr int TILE = PER * ST_WG;
+    __shared__ uint64_t sk[TILE];         // the tile's keys in digit order
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t row = blockIdx.x / tpr, tile = blockIdx.x - row * tpr;  // (tile within the row)
-    const int lim = (int) min((uint32_t) SORT_TILE, row_len - tile * SORT_TILE);
-    const uint64_t* __restrict__ src = in + (size_t) row * row_len + (size_t) tile * SORT_TILE;
+    const int lim = (int) min((uint32_t) TILE, row_len - tile * TILE);
+    const uint64_t* __restrict__ src = in + (size_t) row * row_len + (size_t) tile * TILE;
     uint64_t* __restrict__ dst = out + (size_t) row * row_len;
     const uint32_t* __restrict__ rc = counts + (size_t) row * tpr * 256;  // the row's part of the count table
-    uint64_t k[ST_PER];
+    uint64_t k[PER];
 #pragma unroll
-    for (int s = 0; s < ST_PER; ++s) {
-        const int i = tile_offset(wave, s, lane);
+    for (int s = 0; s < PER; ++s) {
+        const int i = tile_offset<PER>(wave, s, lane);
         k[s] = i < lim ? src[i] : 0ull;
     }
     for (int i = tid; i < ST_NW * 256; i += ST_WG) (&cw[0][0])[i] = 0u;
@@ -114,10 +119,10 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
         tb[tid] += add;
     }
     const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t rk[ST_PER];
+    uint32_t rk[PER];
 #pragma unroll
-    for (int s = 0; s < ST_PER; ++s) {
-        const bool valid = tile_offset(wave, s, lane) < lim;
+    for (int s = 0; s < PER; ++s) {
+        const bool valid = tile_offset<PER>(wave, s, lane) < lim;
         const uint32_t d = rdigit(k[s], shift);
         uint64_t same = ballot64(valid);  // (all lanes take part in every ballot)
 #pragma unroll
@@ -161,8 +166,8 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     __syncthreads();
     // the tile's keys in digit order (stable: wave, then slot, then lane order within a digit)
 #pragma unroll
-    for (int s = 0; s < ST_PER; ++s) {
-        if (tile_offset(wave, s, lane) < lim) {
+    for (int s = 0; s < PER; ++s) {
+        if (tile_offset<PER>(wave, s, lane) < lim) {
             const uint32_t d = rdigit(k[s], shift);
             sk[ts[d] + cw[wave][d] + rk[s]] = k[s];
         }
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     // slot i of the tile goes to the row's slot of its digit: the digit's first row slot for this tile plus its
     // place in the digit's run
 #pragma unroll
-    for (int s = 0; s < ST_PER; ++s) {
+    for (int s = 0; s < PER; ++s) {
         const int i = s * ST_WG + tid;
         if (i < lim) {
             const uint64_t key = sk[i];
@@ -182,21 +187,18 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
     }
 }
 
-}  // namespace
-
-hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
-                          uint32_t* counts, uint64_t** result, hipStream_t s) {
-    if (rows < 1 || row_len == 0 || (size_t) rows * row_len >= (1ull << 32) || begin_bit < 0 ||
-        end_bit <= begin_bit || end_bit > 64)
-        return hipErrorInvalidValue;
-    const uint32_t tpr = (uint32_t) sort_tiles(row_len);
+template <int PER>
+hipError_t sort_passes(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
+                       uint32_t* counts, uint64_t** result, hipStream_t s) {
+    const uint32_t tpr = (uint32_t) ((row_len + PER * ST_WG - 1) / (PER * ST_WG));
     const dim3 grid((unsigned) rows * tpr);
     uint64_t* src = a;
     uint64_t* dst = b;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
-        hipLaunchKernelGGL(sort_hist_kernel, grid, dim3(ST_WG), 0, s, src, (uint32_t) row_len, tpr, shift, counts);
-        hipLaunchKernelGGL(sort_scatter_kernel, grid, dim3(ST_WG), 0, s, src, dst, (uint32_t) row_len, tpr, shift,
+        hipLaunchKernelGGL(sort_hist_kernel<PER>, grid, dim3(ST_WG), 0, s, src, (uint32_t) row_len, tpr, shift,
                            counts);
+        hipLaunchKernelGGL(sort_scatter_kernel<PER>, grid, dim3(ST_WG), 0, s, src, dst, (uint32_t) row_len, tpr,
+                           shift, counts);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         uint64_t* t = src;
@@ -205,6 +207,30 @@ hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, in
     }
     *result = src;
     return hipSuccess;
+}
+
+}  // namespace
+
+// Keys per tile: the largest of 8,192 / 4,096 whose grid (rows x tiles) still covers the CUs (240 workgroups
+// or more), else 2,048. Smaller tiles spread a pass over more CUs, larger ones sum fewer count-table rows per
+// tile (248,320 keys, no top-k limit, device time per step: 4 rows 146.1 / 128.5 / 131.4 us and 1 row 116.7 /
+// 98.8 / 93.9 us with 8,192 / 4,096 / 2,048 keys per tile).
+int sort_tile_keys(int rows, size_t row_len) {
+    for (int t = 8192; t > SORT_TILE_MIN; t >>= 1)
+        if ((size_t) rows * ((row_len + t - 1) / t) >= 240) return t;
+    return SORT_TILE_MIN;
+}
+
+hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
+                          uint32_t* counts, uint64_t** result, hipStream_t s) {
+    if (rows < 1 || row_len == 0 || (size_t) rows * row_len >= (1ull << 32) || begin_bit < 0 ||
+        end_bit <= begin_bit || end_bit > 64)
+        return hipErrorInvalidValue;
+    switch (sort_tile_keys(rows, row_len)) {
+        case 8192: return sort_passes<8>(a, b, rows, row_len, begin_bit, end_bit, counts, result, s);
+        case 4096: return sort_passes<4>(a, b, rows, row_len, begin_bit, end_bit, counts, result, s);
+        default: return sort_passes<2>(a, b, rows, row_len, begin_bit, end_bit, counts, result, s);
+    }
 }
 
 }  // namespace kls
