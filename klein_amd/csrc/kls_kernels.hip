@@ -1478,11 +1478,15 @@ __global__ void expf_table_kernel(uint32_t lo, long long n, float* out) {
 // device-wide radix sort (kls_sort.hip), then the tail over the sorted keys.
 
 constexpr int WIDE_WG = 256;
-constexpr int WIDE_SEG = 4096;  // ids per keys workgroup (32-bit history counts: 16 KB of LDS)
+// ids per keys workgroup: with penalties 4,096 (32-bit history counts: 16 KB of LDS; every workgroup scans the
+// row's history), without 1,024 (4 per thread: four times the workgroups in flight for what is a streaming copy)
+template <bool PENALIZE>
+constexpr int wide_seg() { return PENALIZE ? 4096 : 1024; }
 
 // Keys of ids [lo, hi) of one row (workgroup = (row, segment)), every history count applied to its logit.
 template <bool PENALIZE>
 __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs w) {
+    constexpr int WIDE_SEG = wide_seg<PENALIZE>();
     const int segs = (a.V + WIDE_SEG - 1) / WIDE_SEG;
     const int row = (int) blockIdx.x / segs, seg = (int) blockIdx.x - row * segs;
     const int lo = seg * WIDE_SEG, hi = min(a.V, lo + WIDE_SEG);
@@ -1506,13 +1510,25 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
 
     const uint32_t idm = (1u << ib) - 1u;
     uint64_t* __restrict__ out = w.keys + (int64_t) row * a.V;
-    for (int id = lo + (int) threadIdx.x; id < hi; id += WIDE_WG) {
-        float x = L[id];
-        if (PENALIZE) {
-            const uint32_t c = s_cnt[id - lo];
-            if (c != 0u) x = penalize(x, c, a.p);
+    // the thread's logits are loaded together (a loop of load, wait, store took one memory latency per id)
+    constexpr int PT = WIDE_SEG / WIDE_WG;
+    float v[PT];
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+        const int id = lo + (int) threadIdx.x + j * WIDE_WG;
+        v[j] = id < hi ? L[id] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+        const int id = lo + (int) threadIdx.x + j * WIDE_WG;
+        if (id < hi) {
+            float x = v[j];
+            if (PENALIZE) {
+                const uint32_t c = s_cnt[id - lo];
+                if (c != 0u) x = penalize(x, c, a.p);
+            }
+            out[id] = ((uint64_t) ord_f32(x) << ib) | (uint64_t) (~(uint32_t) id & idm);
         }
-        out[id] = ((uint64_t) ord_f32(x) << ib) | (uint64_t) (~(uint32_t) id & idm);
     }
 }
 
@@ -2887,12 +2903,15 @@ int wide_id_bits(int V) {
 
 hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipStream_t s) {
     if (w.k <= KCAP || w.k > a.V || w.chunks != (w.k + WT_CHUNK - 1) / WT_CHUNK) return hipErrorInvalidValue;
-    const int segs = (a.V + WIDE_SEG - 1) / WIDE_SEG;
-    const dim3 grid((unsigned) (a.n_rows * segs));
-    if (penalize)
-        hipLaunchKernelGGL(wide_keys_kernel<true>, grid, dim3(WIDE_WG), WIDE_SEG * sizeof(uint32_t), s, a, w);
-    else
-        hipLaunchKernelGGL(wide_keys_kernel<false>, grid, dim3(WIDE_WG), 0, s, a, w);
+    if (penalize) {
+        constexpr int SEG = wide_seg<true>();
+        hipLaunchKernelGGL(wide_keys_kernel<true>, dim3((unsigned) (a.n_rows * ((a.V + SEG - 1) / SEG))), dim3(WIDE_WG),
+                           SEG * sizeof(uint32_t), s, a, w);
+    } else {
+        constexpr int SEG = wide_seg<false>();
+        hipLaunchKernelGGL(wide_keys_kernel<false>, dim3((unsigned) (a.n_rows * ((a.V + SEG - 1) / SEG))),
+                           dim3(WIDE_WG), 0, s, a, w);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     uint64_t* sorted = nullptr;
