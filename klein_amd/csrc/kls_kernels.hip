@@ -2172,8 +2172,12 @@ __global__ __launch_bounds__(WT_WG) void wt_probs_kernel(RowsArgs a, WideArgs w)
     const uint64_t fb = ballot(fail != 0x7fffffff);
     if (fb) {
         int m = fail;
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) m = min(m, __shfl_xor(m, d, 64));
+        m = min(m, xor_lane<32>(m, lane));
+        m = min(m, xor_lane<16>(m, lane));
+        m = min(m, xor_lane<8>(m, lane));
+        m = min(m, xor_lane<4>(m, lane));
+        m = min(m, xor_lane<2>(m, lane));
+        m = min(m, xor_lane<1>(m, lane));
         if (lane == 0) atomicMin(&w.rowst[row].n_mp, m);
     }
     if (tid == 0) w.part[(int64_t) row * w.chunks + c] = s;
@@ -2237,7 +2241,7 @@ __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) 
         code[q] = (j0 + q >= n || past) ? CODE_NONE : (easy && !cr) ? E : CODE_HARD;
     }
     // segment heads: the chunk's first term, a term on its own, and a term after one or in another binade
-    int prev = __shfl_up(code[WT_PT - 1], 1, 64);
+    int prev = __builtin_amdgcn_update_dpp(0, code[WT_PT - 1], 0x138, 0xf, 0xf, false);  // wave_shr:1 (lane 0: below)
     if (lane == 63) s_wt_code[wave] = code[WT_PT - 1];
     bool head[WT_PT];
     int hc = 0;
@@ -2251,15 +2255,10 @@ __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) 
     }
     // whether the next term starts a segment or is left out (for a thread's last term: the next thread's first)
     const int brk0 = (head[0] || code[0] == CODE_NONE) ? 1 : 0;
-    int nh = __shfl_down(brk0, 1, 64);
+    int nh = __builtin_amdgcn_update_dpp(0, brk0, 0x130, 0xf, 0xf, false);  // wave_shl:1 (lane 63: below)
     if (lane == 0) s_wt_head[wave] = brk0;
     // segment ordinals: an inclusive scan of the heads
-    int hi = hc;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(hi, d, 64);
-        hi += lane >= d ? y : 0;
-    }
+    const int hi = wave_scan_i32(hc);
     if (lane == 63) s_wt_hcnt[wave] = hi;
     // segmented scan of the maps: each thread's summary, then the wave's and the waves'
     ParMap T = par_identity();
@@ -2349,12 +2348,7 @@ __device__ double wt_resolve(const RowsArgs& a, const WideArgs& w, int row, cons
         // scanned (s_wt_off: the chunks' first records), then as many chunks as fit (at least one)
         __syncthreads();
         const int cnt = cb + tid < nc ? nseg[cb + tid] : 0;
-        int cs = cnt;  // inclusive scan of the counts
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int y = __shfl_up(cs, d, 64);
-            cs += lane >= d ? y : 0;
-        }
+        int cs = wave_scan_i32(cnt);  // inclusive scan of the counts
         if (lane == 63) s_wt_wsum[wave] = cs;
         __syncthreads();
 #pragma unroll
