@@ -27,6 +27,22 @@ __device__ __forceinline__ uint32_t rdigit(uint64_t k, int shift) { return 255u 
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
+// Inclusive prefix sum across the wave, every lane active: row_shr 1, 2, 4, 8 within rows of 16 lanes, then the
+// row broadcasts of lanes 15 and 31 (a source lane outside the row adds 0).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) x, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+    x += dpp_u32<0x111, 0xf>(x);
+    x += dpp_u32<0x112, 0xf>(x);
+    x += dpp_u32<0x114, 0xf>(x);
+    x += dpp_u32<0x118, 0xf>(x);
+    x += dpp_u32<0x142, 0xa>(x);
+    x += dpp_u32<0x143, 0xc>(x);
+    return x;
+}
+
 // Offset of key s of this thread in its tile (wave-major: each wave holds 64 * PER consecutive keys).
 template <int PER>
 __device__ __forceinline__ int tile_offset(int wave, int s, int lane) { return wave * (PER * 64) + s * 64 + lane; }
@@ -102,12 +118,7 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
         // digit totals over every tile, scanned over the digits (4 waves of 64); plus the earlier tiles' counts
         const uint32_t before = part[0][0][tid] + part[0][1][tid] + part[0][2][tid] + part[0][3][tid];
         const uint32_t all = part[1][0][tid] + part[1][1][tid] + part[1][2][tid] + part[1][3][tid];
-        uint32_t x = all;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t y = (uint32_t) __shfl_up((int) x, (unsigned) d, 64);
-            x += lane >= d ? y : 0u;
-        }
+        const uint32_t x = wave_scan_u32(all);
         if (lane == 63) wsum[wave] = x;
         tb[tid] = x - all + before;  // (the earlier waves' totals are added below)
     }
@@ -147,12 +158,7 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
             cw[w][tid] = run;
             run += v;
         }
-        uint32_t x = run;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t y = (uint32_t) __shfl_up((int) x, (unsigned) d, 64);
-            x += lane >= d ? y : 0u;
-        }
+        const uint32_t x = wave_scan_u32(run);
         if (lane == 63) wsum2[wave] = x;
         tile_before = x - run;
     }
