@@ -56,18 +56,22 @@ __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __rest
     constexpr int TILE = PER * ST_WG;
     const int lim = (int) min((uint32_t) TILE, row_len - t * TILE);  // keys in this tile
     const uint64_t* __restrict__ src = in + (size_t) row * row_len + (size_t) t * TILE;
-    if (tid < 256) h[tid] = 0u;
-    __syncthreads();
+    uint64_t k[PER];  // (loaded together, before the table is cleared)
 #pragma unroll
     for (int s = 0; s < PER; ++s) {
         const int i = tile_offset<PER>(wave, s, lane);
-        if (i < lim) atomicAdd(&h[rdigit(src[i], shift)], 1u);
+        k[s] = i < lim ? src[i] : 0ull;
     }
+    if (tid < 256) h[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < PER; ++s)
+        if (tile_offset<PER>(wave, s, lane) < lim) atomicAdd(&h[rdigit(k[s], shift)], 1u);
     __syncthreads();
     if (tid < 256) counts[(size_t) blockIdx.x * 256 + tid] = h[tid];
 }
 
-constexpr int SC_UNROLL = 8;  // count-table rows in flight per thread
+constexpr int SC_UNROLL = 16;  // count-table rows in flight per thread
 
 template <int PER>
 __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
