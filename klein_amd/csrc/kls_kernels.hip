@@ -2195,10 +2195,21 @@ __global__ __launch_bounds__(WT_WG) void wt_maps_kernel(RowsArgs a, WideArgs w) 
     const double* t = wide_terms(a, w, row);
     const int j0 = lo + tid * WT_PT;
     double sv[WT_PT];  // the terms as the chain adds them (0 past n)
+    static_assert(WT_PT % 2 == 0, "pairs of terms");
+    if (j0 + WT_PT <= n && (reinterpret_cast<uintptr_t>(t) & 15u) == 0) {
+        // 16-byte loads (j0 is a multiple of WT_PT; the row's terms start 16-byte aligned when V is even)
 #pragma unroll
-    for (int q = 0; q < WT_PT; ++q) {
-        const double x = t[min(j0 + q, n - 1)];
-        sv[q] = j0 + q < n ? (ch.NEG ? -x : x) : 0.0;
+        for (int q = 0; q < WT_PT; q += 2) {
+            const double2 x = *reinterpret_cast<const double2*>(t + j0 + q);
+            sv[q] = ch.NEG ? -x.x : x.x;
+            sv[q + 1] = ch.NEG ? -x.y : x.y;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < WT_PT; ++q) {
+            const double x = t[min(j0 + q, n - 1)];
+            sv[q] = j0 + q < n ? (ch.NEG ? -x : x) : 0.0;
+        }
     }
     // approximate partial results: the earlier chunks' sums, then an exclusive scan of the threads' sums
     double pre = 0.0, all = 0.0, own = 0.0;
