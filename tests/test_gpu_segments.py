@@ -108,6 +108,21 @@ def test_segment_lengths_batch(torch_cuda, K, oracle_lib, seg):
         check_batch(torch, K, oracle_lib, x, p, hists, u, seg, f"V{V} T{T} k{k} pen{pen}")
 
 
+def test_greedy_batch_rows_not_whole_float4s(torch_cuda, K, oracle_lib):
+    """64 greedy rows with penalties whose logits are not whole float4s (V = 248,319, contiguous rows): the
+    default layout keeps such greedy launches to 32,768-id segments (the 65,536-id form of that kernel spills
+    registers); tokens against the oracle with the default layout and with 65,536-id segments forced."""
+    torch = torch_cuda
+    rng = np.random.default_rng(31)
+    V, rows = 248319, 64
+    x = head_rows(rng, rows, V)
+    p = W.Params(temperature=0.0, presence_penalty=0.5, frequency_penalty=0.2, repetition_penalty=1.1)
+    hists = [np.concatenate([zipf_history(rng, V, 4000), np.argsort(-x[r])[:20].astype(np.int32)])
+             for r in range(rows)]
+    for seg in (0, 65536):
+        check_batch(torch, K, oracle_lib, x, p, hists, np.zeros(rows), seg, "greedy rows not whole float4s")
+
+
 @pytest.mark.parametrize("seg", (16384, 65536, 4096))
 def test_history_counts_above_16_bits(torch_cuda, K, oracle_lib, seg):
     """A row whose history holds 70,000 ids, one id 66,000 times: 16-bit count tables would wrap, so the kernel
