@@ -2754,15 +2754,37 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
     if (tid == 0) s_mid_base = (int) atomicAdd(&m.fill[row], (uint32_t) total);
     __syncthreads();
     uint64_t* const buf = m.buf + (int64_t) row * MID_ROWCAP;
-    int o = s_mid_base + off;
+    // The keys are placed in LDS in thread order first (the count table and the sort space are free here), then
+    // written to the row's buffer with neighbouring threads on neighbouring slots: straight from the registers,
+    // each thread's 32 conditional stores were 32 store instructions per wave for a few keys each, all waited for
+    // before the ticket. A few keys (at most 256: the extra barrier costs more than the stores save), or no room
+    // in LDS (one segment, a larger cap), are stored directly.
+    constexpr int STAGE = PENALIZE ? MID_SEG * (int) sizeof(uint32_t) / 8 : 2 * MID_SORT;  // keys the LDS holds
+    if (total > 256 && total <= STAGE) {  // (uniform)
+        uint64_t* const stage = reinterpret_cast<uint64_t*>(s_cnt);
+        int o = off;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
+        for (int i = 0; i < NV; ++i) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint64_t key = mk_key(v[4 * i + e], lo + 4 * (i * WG + tid) + e);
-            if (key >= T) {
-                if (o < MID_ROWCAP) store_dev(&buf[o], key);
-                ++o;
+            for (int e = 0; e < 4; ++e) {
+                const uint64_t key = mk_key(v[4 * i + e], lo + 4 * (i * WG + tid) + e);
+                if (key >= T) stage[o++] = key;
+            }
+        }
+        __syncthreads();
+        for (int j = tid; j < total; j += WG)
+            if (s_mid_base + j < MID_ROWCAP) store_dev(&buf[s_mid_base + j], stage[j]);
+    } else {
+        int o = s_mid_base + off;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint64_t key = mk_key(v[4 * i + e], lo + 4 * (i * WG + tid) + e);
+                if (key >= T) {
+                    if (o < MID_ROWCAP) store_dev(&buf[o], key);
+                    ++o;
+                }
             }
         }
     }
