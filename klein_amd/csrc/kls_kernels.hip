@@ -2531,12 +2531,19 @@ __shared__ int s_mid_c[2][MID_NW];    // per-wave counts (two sets, used alterna
 __shared__ int s_mid_base;
 
 // The j-th largest (1 <= j <= 64) of the 128 values m1, m2 of the wave's lanes (value images, m2 <= m1 in each
-// lane); 0 when fewer than j are nonzero.
+// lane); 0 when fewer than j are nonzero. It is the largest t that at least j of the values reach, built from
+// the top bit down: per bit two compares, whose lane masks are the ballots, and scalar counts (a chain of 32
+// short steps; two 64-lane bitonic sorts and a merge were 48 dependent cross-lane steps).
 __device__ __forceinline__ uint32_t wave_top2_kth(uint32_t m1, uint32_t m2, int j, int lane) {
-    const uint32_t a = sort32<true>(m1, lane);
-    const uint32_t b = sort32<false>(m2, lane);
-    const uint32_t c = merge32(a, b, lane);  // the top 64 of the union, descending
-    return (uint32_t) rdlanei((int) c, j - 1);
+    (void) lane;
+    uint32_t t = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t c = t | (1u << b);
+        const int n = __popcll(ballot(m1 >= c)) + __popcll(ballot(m2 >= c));
+        t = n >= j ? c : t;
+    }
+    return t;
 }
 
 // Workgroup sum of c (every thread calls it). `par` alternates the LDS slots, so one barrier per call suffices:
