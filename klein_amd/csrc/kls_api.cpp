@@ -171,6 +171,7 @@ struct kls_sampler {
     const float* g_logits = nullptr;
     int g_rows = 0;
     bool g_count_wide = false;
+    bool g_verify = false;          // the captured step is a verify step (else a one-row sample on the wide path)
     bool g_valid = false;
     RowsArgs g_args{};  // the arguments the verify graph was captured with
 };
@@ -420,8 +421,12 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
     if (st) return st;
     h->call->seq = ++h->seq;
     const RowsArgs a = step_args(h, dl, rows, verify);
-    if (verify) {
-        if (!h->g_valid || h->g_logits != dl || h->g_rows != rows) {
+    // A verify step is one graph launch; so is a sample on the wide path, whose keys, radix passes and tail are
+    // many kernels (one graph launch costs the host less than their direct launches). A fast- or mid-path sample is
+    // one kernel, launched directly. The graph is kept while the logits pointer, the row count and the kind of
+    // step stay the same.
+    if (verify || h->wide) {
+        if (!h->g_valid || h->g_logits != dl || h->g_rows != rows || h->g_verify != verify) {
             // (a stale graph is replaced whether or not its teardown reports an error)
             if (h->gexec) (void) hipGraphExecDestroy(h->gexec);
             if (h->graph) (void) hipGraphDestroy(h->graph);
@@ -443,6 +448,7 @@ int enqueue_step(kls_sampler* h, const float* logits, int rows, bool verify, hip
             h->g_logits = dl;
             h->g_rows = rows;
             h->g_count_wide = h->count_wide;
+            h->g_verify = verify;
             h->g_args = a;
             h->g_valid = true;
         }
@@ -862,7 +868,7 @@ int kls_debug_time_verify(kls_handle h, int n, int reps, kls_stream stream, doub
     if (int st = check_handle(h)) return st;
     if (n < 1 || reps < 1 || !out_us) return fail(KLS_ERR_INVALID_ARG, "bad arguments");
     if (h->inflight) return fail(KLS_ERR_INVALID_ARG, "a step is in flight on this handle");
-    if (!h->g_valid) return fail(KLS_ERR_INVALID_ARG, "no captured verify step on this handle");
+    if (!h->g_valid || !h->g_verify) return fail(KLS_ERR_INVALID_ARG, "no captured verify step on this handle");
     (void) hipSetDevice(h->device);
     hipStream_t s = stream ? (hipStream_t) stream : h->stream;
     if (int st = order_on(h, s)) return st;

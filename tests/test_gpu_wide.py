@@ -274,6 +274,43 @@ def test_wide_sort_tile_edges(torch_cuda, K, oracle_lib, V):
     S.close()
 
 
+def test_wide_sample_graph_alternates_with_verify(torch_cuda, K, oracle_lib):
+    """One-row samples without a top-k limit are one graph launch too, kept while the logits pointer, the row
+    count and the kind of step stay the same: samples from two device buffers, a verify step between them (its own
+    graph), then samples again, each against the oracle."""
+    O = oracle_lib
+    torch = torch_cuda
+    V, nb = 70001, 4
+    rng = np.random.default_rng(91)
+    p = W.Params(temperature=0.8, top_k=0, top_p=0.9, seed=5)
+    S = K.Sampler(p, n_vocab=V, max_rows=nb)
+    assert S.path == "wide"
+    xa, xb = head_rows(rng, nb, V), head_rows(rng, 1, V)
+    da, db = dev(torch, xa), dev(torch, xb)
+    counts = np.zeros(V, np.int32)
+
+    def one(d, xr, tag):
+        u = float(rng.random())
+        say("wide sample graph", tag)
+        got = S.sample(d, u=u)
+        assert got == O.sample(xr, p, u, counts, O.MODE_TOTAL)[0], tag
+
+    for i in range(2):
+        one(da[0], xa[0], f"buffer a {i}")
+    for i in range(2):
+        one(db[0], xb[0], f"buffer b {i}")
+    u = rng.random(nb)
+    drafts = np.array([O.sample(xa[0], p, u[0], counts, O.MODE_TOTAL)[0]] + list(rng.integers(0, V, nb - 2)),
+                      np.int32)
+    say("wide verify between samples")
+    toks, acc = S.verify(da, drafts, u=u)
+    ot, oa, _ = O.verify(xa, drafts, p, u, counts, O.MODE_TOTAL)
+    assert acc == oa and list(toks) == list(ot[:oa + 1]), (acc, oa)
+    one(da[0], xa[0], "buffer a after verify")
+    one(db[0], xb[0], "buffer b after verify")
+    S.close()
+
+
 def test_wide_verify_steps_captured(torch_cuda, K, oracle_lib):
     """Verify steps without a top-k limit are one graph launch like the others (keys, the sort's passes and the
     tail captured together): five steps against the oracle, then the graph timed by its hook."""
