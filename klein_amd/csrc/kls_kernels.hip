@@ -2520,6 +2520,7 @@ __global__ __launch_bounds__(TAIL_WG) void wt_resolve_kernel(RowsArgs a, WideArg
 // Counters are left zero for the next launch (the ticket by publish, the buffer's counter by the last workgroup).
 constexpr int MID_NW = 16, MID_WG = MID_NW * 64, MID_EPT = 32, MID_RK = MID_ROWCAP / MID_WG;
 constexpr int MID_SORT = 4096;  // keys the row's sort holds
+constexpr int MID_BIGK = 256;   // top-k above this takes the kernel with the register-templated sort
 static_assert(MID_WG * MID_EPT == MID_SEG, "segment length");
 static_assert(MID_WG == TAIL_WG, "the row's tail runs on the mid workgroup");
 static_assert(MID_KMAX <= TAIL_WG, "sorted_tail holds one candidate per thread");
@@ -2672,7 +2673,84 @@ __device__ __forceinline__ int mid_sort(int P, int lane, int wave) {
     return bo;
 }
 
-template <bool PENALIZE>
+// The same sort with the registers that hold elements as a template parameter (NR = P / 1024, at least 1; with 1,
+// the waves past P / 64 hold none and only take the barriers): every register is live, so an exchange's LDS reads
+// are issued together and waited for once, where the form above makes each register's test its own block with its
+// own wait (2,048 keys timed alone: 9.6 against 13.4 us). It has its own kernel instantiation for large top-k: in
+// the same kernel as the form above it changed the compiler's schedule of the segment phase and cost small k more
+// than it saved.
+template <int NR>
+__device__ __forceinline__ int mid_sort_r(int P, int lane, int wave) {
+    static_assert(NR >= 1 && NR * MID_WG <= MID_SORT, "registers per thread");
+    uint64_t* const L = reinterpret_cast<uint64_t*>(s_cnt);
+    const bool act = NR > 1 || wave < (P >> 6);  // (uniform in the wave)
+    uint64_t x[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) x[r] = act ? L[(r * MID_NW + wave) * 64 + lane] : 0ull;
+    if (act) {
+        // chunks alternately descending and ascending: every block of 128 is then bitonic
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            x[r] = ((r * MID_NW + wave) & 1) ? sort64<false>(x[r], lane) : sort64<true>(x[r], lane);
+    }
+    int bo = MID_SORT;  // the half the next exchange writes (U first, then alternating)
+    for (int size = 128; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride >= 64; stride >>= 1) {
+            if (stride >= MID_WG) {
+                const int rs = stride / MID_WG;
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    const int r2 = r | rs;
+                    if ((r & rs) == 0 && r2 < NR) {
+                        const bool desc = (((r * MID_NW + wave) * 64) & size) == 0;
+                        const uint64_t mx = max64(x[r], x[r2]), mn = min64(x[r], x[r2]);
+                        x[r] = desc ? mx : mn;
+                        x[r2] = desc ? mn : mx;
+                    }
+                }
+            } else {
+                const int b = bo;
+                bo ^= MID_SORT;
+                if (act) {
+#pragma unroll
+                    for (int r = 0; r < NR; ++r) L[b + (r * MID_NW + wave) * 64 + lane] = x[r];
+                }
+                __syncthreads();
+                if (act) {
+                    uint64_t y[NR];
+#pragma unroll
+                    for (int r = 0; r < NR; ++r) y[r] = L[b + (((r * MID_NW + wave) * 64 + lane) ^ stride)];
+#pragma unroll
+                    for (int r = 0; r < NR; ++r) {
+                        const int i = (r * MID_NW + wave) * 64 + lane;
+                        const bool lower = (i & stride) == 0, desc = (i & size) == 0;
+                        x[r] = (lower == desc) ? max64(x[r], y[r]) : min64(x[r], y[r]);
+                    }
+                }
+            }
+        }
+        if (act) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                x[r] = (((r * MID_NW + wave) * 64) & size) == 0 ? bitonic_stage<64, true>(x[r], lane)
+                                                                 : bitonic_stage<64, false>(x[r], lane);
+        }
+    }
+    if (act) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) L[bo + (r * MID_NW + wave) * 64 + lane] = x[r];
+    }
+    __syncthreads();
+    return bo;
+}
+
+__device__ __forceinline__ int mid_sort_big(int P, int lane, int wave) {
+    static_assert(MID_SORT == 4 * MID_WG, "at most four registers per thread");
+    return P > 2 * MID_WG ? mid_sort_r<4>(P, lane, wave)
+                          : P > MID_WG ? mid_sort_r<2>(P, lane, wave) : mid_sort_r<1>(P, lane, wave);
+}
+
+template <bool PENALIZE, bool BIGK>
 __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
     constexpr int WG = MID_WG, EPT = MID_EPT, NV = EPT / 4;
     const int tid = (int) threadIdx.x, lane = lane_id(), wave = tid >> 6;
@@ -2863,7 +2941,9 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
         }
     }
     __syncthreads();
-    const int ko = mid_sort(P, lane, wave);
+    int ko;
+    if constexpr (BIGK) ko = mid_sort_big(P, lane, wave);
+    else ko = mid_sort(P, lane, wave);
     sorted_tail(a, row, S + ko, min(k, n2), reinterpret_cast<double*>(S + (MID_SORT - ko)), cin, FastKeyFmt{});
 }
 
@@ -2976,19 +3056,29 @@ hipError_t launch_mid(const RowsArgs& a, const MidArgs& m, bool penalize, hipStr
         (int64_t) m.cap * a.segs > MID_ROWCAP)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned) (a.n_rows * a.segs));
-    if (penalize)
-        hipLaunchKernelGGL(mid_kernel<true>, grid, dim3(MID_WG), MID_SEG * sizeof(uint32_t), s, a, m);
-    else
-        hipLaunchKernelGGL(mid_kernel<false>, grid, dim3(MID_WG), 2 * MID_SORT * sizeof(uint64_t), s, a, m);
+    // top-k above MID_BIGK: the instantiation with the register-templated sort (k = 512 / 1,024: -1.0 / -2.2 us;
+    // at k = 65 / 256 that instantiation is 0.9 / 0.2 us slower, its segment phase scheduled differently)
+    const size_t lp = MID_SEG * sizeof(uint32_t), ln = 2 * MID_SORT * sizeof(uint64_t);
+    if (m.k > MID_BIGK) {
+        if (penalize) hipLaunchKernelGGL((mid_kernel<true, true>), grid, dim3(MID_WG), lp, s, a, m);
+        else hipLaunchKernelGGL((mid_kernel<false, true>), grid, dim3(MID_WG), ln, s, a, m);
+    } else {
+        if (penalize) hipLaunchKernelGGL((mid_kernel<true, false>), grid, dim3(MID_WG), lp, s, a, m);
+        else hipLaunchKernelGGL((mid_kernel<false, false>), grid, dim3(MID_WG), ln, s, a, m);
+    }
     return hipGetLastError();
 }
 
 hipError_t prepare_mid_kernels() {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mid_kernel<true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int) (MID_SEG * sizeof(uint32_t)));
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mid_kernel<false>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * MID_SORT * sizeof(uint64_t)));
+    const int lp = (int) (MID_SEG * sizeof(uint32_t)), ln = (int) (2 * MID_SORT * sizeof(uint64_t));
+    const void* k[4] = {reinterpret_cast<const void*>(&mid_kernel<true, false>),
+                        reinterpret_cast<const void*>(&mid_kernel<true, true>),
+                        reinterpret_cast<const void*>(&mid_kernel<false, false>),
+                        reinterpret_cast<const void*>(&mid_kernel<false, true>)};
+    const int lds[4] = {lp, lp, ln, ln};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 4 && e == hipSuccess; ++i)
+        e = hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize, lds[i]);
     return e;
 }
 
