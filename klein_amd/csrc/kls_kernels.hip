@@ -2941,9 +2941,11 @@ __global__ __launch_bounds__(MID_WG) void mid_kernel(RowsArgs a, MidArgs m) {
         }
     }
     __syncthreads();
+    // (top-k <= 256: the one-register form up to 1,024 keys, else the generic one; together they add less code to
+    // this kernel than the templated forms, whose size changed the segment phase's schedule)
     int ko;
     if constexpr (BIGK) ko = mid_sort_big(P, lane, wave);
-    else ko = mid_sort(P, lane, wave);
+    else ko = P <= MID_WG ? mid_sort_r<1>(P, lane, wave) : mid_sort(P, lane, wave);
     sorted_tail(a, row, S + ko, min(k, n2), reinterpret_cast<double*>(S + (MID_SORT - ko)), cin, FastKeyFmt{});
 }
 
