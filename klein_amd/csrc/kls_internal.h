@@ -128,7 +128,7 @@ constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 20;
 // after every number. The sorted keys then go through the O(k) tail in reference order.
 // The wide path's tail cuts each of its double chains into chunks of WT_CHUNK terms (kls_kernels.hip), and each
 // chunk into at most WT_SEGS segments, recorded in order:
-constexpr int WT_CHUNK = 2048, WT_SEGS = 64;
+constexpr int WT_CHUNK = 1024, WT_SEGS = 64;
 enum : int32_t {
     WS_MAP = 1,     // terms [start, end) composed to one parity map in the binade 2^E
     WS_TERM = 2,    // one term (d0, signed as the chain adds it) added on its own

@@ -1643,8 +1643,8 @@ __device__ __forceinline__ ParMap term_map(double t, int E, double* f, bool* cro
 // together, so a block waits for one memory latency, not one per term), composes their maps, and the workgroup
 // scans the threads' maps, so a block covers TAIL_WG * RP_PT terms with one scan and two barriers; each thread
 // then walks its own terms from the scanned prefix to find the first that leaves the binade or meets the stop.
-// 1 suits chains of at most TAIL_WG terms (no serial walk: the mid path's tail), 2 the wide tail's chunks of
-// 2 * TAIL_WG terms.
+// 1 suits chains of at most TAIL_WG terms (no serial walk: the mid path's tail and the wide tail's chunks), 2
+// chains of up to 2 * TAIL_WG terms.
 // NEG: the chain adds -t_i (the draw's subtractions) instead of t_i.
 template <int RP_PT, bool NEG = false, typename F>
 __device__ double replay_sum(const double* __restrict__ t, int n, double acc, F stop, int* stopped) {
@@ -2040,7 +2040,8 @@ __device__ void sorted_tail(const RowsArgs& a, int row, const uint64_t* K, int k
 constexpr int WT_WG = 256, WT_PT = WT_CHUNK / WT_WG;
 constexpr int WT_FLAT = 1400;  // segment records a resolve kernel holds in LDS at once
 static_assert(WT_FLAT >= WT_SEGS, "a window holds at least one chunk's segments");
-static_assert(WT_CHUNK == 2 * TAIL_WG, "a replayed segment is at most one replay_sum block of two terms per thread");
+constexpr int WT_RP = WT_CHUNK > TAIL_WG ? 2 : 1;  // replay_sum terms per thread: a replayed segment (at most a chunk) is one block
+static_assert(WT_CHUNK <= WT_RP * TAIL_WG, "a chunk is one replay_sum block of one or two terms per thread");
 // segment codes of a term on its own / past n or past the stop
 constexpr int CODE_HARD = -0x7fffffff, CODE_NONE = -0x7ffffffe;
 
@@ -2438,7 +2439,7 @@ __device__ double wt_resolve(const RowsArgs& a, const WideArgs& w, int row, cons
             __syncthreads();  // (read before wave 0 rewrites them)
             if (rs < 0) break;  // the window is walked, or the chain stopped
             int s2;
-            acc = replay_sum<2, WtChain<PH>::NEG>(t + rs, re - rs, acc, stop, &s2);
+            acc = replay_sum<WT_RP, WtChain<PH>::NEG>(t + rs, re - rs, acc, stop, &s2);
             if (s2 >= 0) {
                 st = rs + s2;
                 break;

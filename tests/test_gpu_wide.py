@@ -120,7 +120,7 @@ def test_wide_batch(torch_cuda, K, oracle_lib, case):
 # The wide tail's chunked chains: rows whose sums cross many binades over many chunks (flat logits), top-p at 1
 # (no stop), min-p cutting inside a chunk, a k that ends inside a chunk, bf16-valued rows (runs of equal terms),
 # low and high temperatures, uniforms 0.9999999 and 0 (the draw running to the end / stopping at once), and a
-# 3,000,000-entry vocabulary (1,465 chunks: the resolve kernels' segment records in several windows).
+# 3,000,000-entry vocabulary (2,930 chunks: the resolve kernels' segment records in several windows).
 # V, rows, temperature, top_k, top_p, min_p, kind
 CHUNK_CASES = [
     (248320, 3, 1.0, 0, 0.95, 0.0, "flat"),
