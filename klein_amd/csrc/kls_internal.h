@@ -251,9 +251,14 @@ hipError_t prepare_mid_kernels();  // once per device: LDS limit of the kernel w
 // bits [begin_bit, end_bit) (kls_sort.hip): a stable radix sort, 8 bits per pass, alternating between the buffers
 // a (the input) and b; *result is the one that holds the sorted keys. Keys equal on those bits keep their input
 // order. counts: 256 * rows * sort_tiles(row_len) words of scratch (enough for every tile size the sort picks).
+// Each row is cut into tiles of sort_tile_keys(rows, row_len) keys (2,048, 4,096 or 8,192), and a pass's counts
+// are tile-major: counts[(r * tiles_per_row + t) * 256 + 255 - digit] for tile t of row r. first_counted: the
+// caller has written the first pass's counts (bits [begin_bit, begin_bit + 8) of the keys in a) in that layout,
+// and the first pass's histogram kernel is not launched.
 constexpr int SORT_TILE_MIN = 2048;
 inline size_t sort_tiles(size_t n) { return (n + SORT_TILE_MIN - 1) / SORT_TILE_MIN; }
+int sort_tile_keys(int rows, size_t row_len);
 hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
-                          uint32_t* counts, uint64_t** result, hipStream_t s);
+                          uint32_t* counts, bool first_counted, uint64_t** result, hipStream_t s);
 
 }  // namespace kls

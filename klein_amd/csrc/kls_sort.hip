@@ -199,14 +199,15 @@ __global__ __launch_bounds__(ST_WG) void sort_scatter_kernel(const uint64_t* __r
 
 template <int PER>
 hipError_t sort_passes(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
-                       uint32_t* counts, uint64_t** result, hipStream_t s) {
+                       uint32_t* counts, bool first_counted, uint64_t** result, hipStream_t s) {
     const uint32_t tpr = (uint32_t) ((row_len + PER * ST_WG - 1) / (PER * ST_WG));
     const dim3 grid((unsigned) rows * tpr);
     uint64_t* src = a;
     uint64_t* dst = b;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
-        hipLaunchKernelGGL(sort_hist_kernel<PER>, grid, dim3(ST_WG), 0, s, src, (uint32_t) row_len, tpr, shift,
-                           counts);
+        if (!(first_counted && shift == begin_bit))
+            hipLaunchKernelGGL(sort_hist_kernel<PER>, grid, dim3(ST_WG), 0, s, src, (uint32_t) row_len, tpr, shift,
+                               counts);
         hipLaunchKernelGGL(sort_scatter_kernel<PER>, grid, dim3(ST_WG), 0, s, src, dst, (uint32_t) row_len, tpr,
                            shift, counts);
         const hipError_t e = hipGetLastError();
@@ -232,14 +233,14 @@ int sort_tile_keys(int rows, size_t row_len) {
 }
 
 hipError_t sort_keys_desc(uint64_t* a, uint64_t* b, int rows, size_t row_len, int begin_bit, int end_bit,
-                          uint32_t* counts, uint64_t** result, hipStream_t s) {
+                          uint32_t* counts, bool first_counted, uint64_t** result, hipStream_t s) {
     if (rows < 1 || row_len == 0 || (size_t) rows * row_len >= (1ull << 32) || begin_bit < 0 ||
         end_bit <= begin_bit || end_bit > 64)
         return hipErrorInvalidValue;
     switch (sort_tile_keys(rows, row_len)) {
-        case 8192: return sort_passes<8>(a, b, rows, row_len, begin_bit, end_bit, counts, result, s);
-        case 4096: return sort_passes<4>(a, b, rows, row_len, begin_bit, end_bit, counts, result, s);
-        default: return sort_passes<2>(a, b, rows, row_len, begin_bit, end_bit, counts, result, s);
+        case 8192: return sort_passes<8>(a, b, rows, row_len, begin_bit, end_bit, counts, first_counted, result, s);
+        case 4096: return sort_passes<4>(a, b, rows, row_len, begin_bit, end_bit, counts, first_counted, result, s);
+        default: return sort_passes<2>(a, b, rows, row_len, begin_bit, end_bit, counts, first_counted, result, s);
     }
 }
 

@@ -80,6 +80,13 @@ BATCH_CASES = [
     (248320, 2, 1.3, 200, 1.0, 0.0, 0, 0),
     (5000, 3, 2.0, 0, 0.999, 0.0, 0, 0),
     (100, 2, 1.0, 0, 1.0, 0.01, 1, 300),
+    # the sort's larger tiles (the largest of 8,192 / 4,096 keys whose grid reaches 240 workgroups, else 2,048):
+    # 30,001 ids are 4 tiles of 8,192 (the last partial) or 8 of 4,096, so 64 rows sort in tiles of 8,192 and 32
+    # rows in tiles of 4,096, with the keys kernel counting the first digit (no penalties) or the sort (penalties)
+    (30001, 64, 1.0, 0, 0.95, 0.0, 0, 0),
+    (30001, 32, 0.8, 0, 0.9, 0.0, 0, 0),
+    (30001, 64, 1.0, 0, 0.95, 0.0, 1, 500),
+    (30001, 32, 0.8, 0, 0.9, 0.02, 2, 300),
 ]
 
 
@@ -253,8 +260,9 @@ def test_wide_sample_and_verify_with_history(torch_cuda, K, oracle_lib, k):
 
 @pytest.mark.parametrize("V", [8192, 8193, 16385])
 def test_wide_sort_tile_edges(torch_cuda, K, oracle_lib, V):
-    """The radix sort at tile boundaries (8,192 keys a tile: exactly one, one past, two and one past), on rows with
-    all-equal runs (keys that differ in the id bits only) and a row without a limit."""
+    """The radix sort at tile boundaries (one row: tiles of 2,048 keys; 8,192 ids are four whole tiles, 8,193 and
+    16,385 one key past four and eight), on rows with all-equal runs (keys that differ in the id bits only) and a
+    row without a limit."""
     torch = torch_cuda
     O = oracle_lib
     rng = np.random.default_rng(V)
