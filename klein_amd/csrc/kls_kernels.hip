@@ -1483,7 +1483,13 @@ constexpr int WIDE_WG = 256;
 constexpr int WIDE_SEG = 4096;
 
 // Keys of ids [lo, hi) of one row (workgroup = (row, segment)), every history count applied to its logit.
+// TPW: sort tiles per workgroup (1: tiles of 4,096 keys, 2: of 2,048), whose counts of the sort's first digit the
+// workgroup writes as the sort's histogram kernel would (its first histogram launch is then saved); 0: none (tiles
+// of 8,192 keys span two workgroups).
+template <int TPW>
 __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs w) {
+    static_assert(TPW == 0 || (TPW <= 2 && WIDE_SEG / TPW >= SORT_TILE_MIN), "whole sort tiles per workgroup");
+    __shared__ uint32_t h[TPW > 0 ? TPW : 1][256];
     const int segs = (a.V + WIDE_SEG - 1) / WIDE_SEG;
     const int row = (int) blockIdx.x / segs, seg = (int) blockIdx.x - row * segs;
     const int lo = seg * WIDE_SEG, hi = min(a.V, lo + WIDE_SEG);
@@ -1499,6 +1505,8 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
         }
         const int4 none[HR] = {};
         cnt_zero<WIDE_WG>(hi - lo);
+        if (TPW > 0)
+            for (int i = (int) threadIdx.x; i < TPW * 256; i += WIDE_WG) (&h[0][0])[i] = 0u;
         __syncthreads();
         count_history<WIDE_WG, false, false>(a, row, lo, hi, none, rh, (int) threadIdx.x);
         __syncthreads();
@@ -1522,7 +1530,19 @@ __global__ __launch_bounds__(WIDE_WG) void wide_keys_kernel(RowsArgs a, WideArgs
             float x = v[j];
             const uint32_t c = s_cnt[id - lo];
             if (c != 0u) x = penalize(x, c, a.p);
-            out[id] = ((uint64_t) ord_f32(x) << ib) | (uint64_t) (~(uint32_t) id & idm);
+            const uint32_t o = ord_f32(x);
+            out[id] = ((uint64_t) o << ib) | (uint64_t) (~(uint32_t) id & idm);
+            // (the tile of id within the workgroup is j * WIDE_WG / tile: a constant of the unrolled loop)
+            if (TPW > 0) atomicAdd(&h[TPW > 1 ? j * WIDE_WG * TPW / WIDE_SEG : 0][255u - (o & 255u)], 1u);
+        }
+    }
+    if (TPW > 0) {
+        __syncthreads();
+        constexpr int TILE = WIDE_SEG / (TPW > 0 ? TPW : 1);
+        const int tiles = (a.V + TILE - 1) / TILE;  // the row's tiles
+        for (int i = (int) threadIdx.x; i < TPW * 256; i += WIDE_WG) {
+            const int t = seg * TPW + i / 256;
+            if (t < tiles) w.counts[((size_t) row * tiles + t) * 256 + (i & 255)] = (&h[0][0])[i];
         }
     }
 }
@@ -3054,12 +3074,15 @@ int wide_id_bits(int V) {
 
 hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipStream_t s) {
     if (w.k <= KCAP || w.k > a.V || w.chunks != (w.k + WT_CHUNK - 1) / WT_CHUNK) return hipErrorInvalidValue;
+    const int tile = sort_tile_keys(a.n_rows, (size_t) a.V);
     if (penalize) {
-        hipLaunchKernelGGL(wide_keys_kernel, dim3((unsigned) (a.n_rows * ((a.V + WIDE_SEG - 1) / WIDE_SEG))),
-                           dim3(WIDE_WG), WIDE_SEG * sizeof(uint32_t), s, a, w);
+        const dim3 g((unsigned) (a.n_rows * ((a.V + WIDE_SEG - 1) / WIDE_SEG)));
+        constexpr size_t lds = WIDE_SEG * sizeof(uint32_t);
+        if (tile == WIDE_SEG) hipLaunchKernelGGL(wide_keys_kernel<1>, g, dim3(WIDE_WG), lds, s, a, w);
+        else if (tile == WIDE_SEG / 2) hipLaunchKernelGGL(wide_keys_kernel<2>, g, dim3(WIDE_WG), lds, s, a, w);
+        else hipLaunchKernelGGL(wide_keys_kernel<0>, g, dim3(WIDE_WG), lds, s, a, w);
     } else {
         // one workgroup per sort tile, which also counts the sort's first digit
-        const int tile = sort_tile_keys(a.n_rows, (size_t) a.V);
         const dim3 g((unsigned) (a.n_rows * ((a.V + tile - 1) / tile)));
         if (tile == 8192) hipLaunchKernelGGL(wide_keys_hist_kernel<8192>, g, dim3(WKH_WG), 0, s, a, w);
         else if (tile == 4096) hipLaunchKernelGGL(wide_keys_hist_kernel<4096>, g, dim3(WKH_WG), 0, s, a, w);
@@ -3071,7 +3094,8 @@ hipError_t launch_wide(const RowsArgs& a, const WideArgs& w, bool penalize, hipS
     // Each row's keys are sorted on their own. They are written in id order and the sort is stable, so sorting on
     // the value field alone leaves equal values in ascending id order, as the id field would: its passes are
     // skipped (4 passes of 8 bits).
-    e = sort_keys_desc(w.keys, w.sorted, a.n_rows, (size_t) a.V, w.id_bits, 32 + w.id_bits, w.counts, !penalize,
+    const bool counted = !penalize || tile <= WIDE_SEG;  // the keys kernel wrote the first pass's counts
+    e = sort_keys_desc(w.keys, w.sorted, a.n_rows, (size_t) a.V, w.id_bits, 32 + w.id_bits, w.counts, counted,
                        &sorted, s);
     if (e != hipSuccess) return e;
     // the tail reads the sorted buffer and keeps its terms in the other one: the three chains, each mapped per
