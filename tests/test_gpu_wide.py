@@ -98,6 +98,17 @@ def test_wide_batch(torch_cuda, K, oracle_lib, case):
     rng = np.random.default_rng(900 + case)
     x = head_rows(rng, rows, V)
     p = W.Params(temperature=T, top_k=k, top_p=tp, min_p=mp, **PENS[pen])
+    S = K.Sampler(p, n_vocab=V, max_rows=rows)
+    assert S.path == expected_path(V, k), (case, S.path)
+    say("wide batch", case, "V", V, "k", k, "rows", rows, S.path)
+    run_batch(torch, S, O, rng, x, p, pen, nh, f"case{case}")
+    S.close()
+
+
+def run_batch(torch, S, O, rng, x, p, pen, nh, label):
+    """One kls_sample_batch call over the rows of x (with zipf histories of nh ids plus each row's 30 largest
+    logits when pen), every row checked against the oracle."""
+    rows, V = x.shape
     hists = [zipf_history(rng, V, nh) if nh else np.zeros(0, np.int32) for _ in range(rows)]
     if pen:
         for r in range(rows):  # push some heads through the penalties
@@ -107,10 +118,7 @@ def test_wide_batch(torch_cuda, K, oracle_lib, case):
     ids = np.concatenate(hists).astype(np.int32) if off[-1] else np.zeros(1, np.int32)
     u = rng.random(rows)
     u[0] = 0.9999999
-    S = K.Sampler(p, n_vocab=V, max_rows=rows)
-    assert S.path == expected_path(V, k), (case, S.path)
     out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
-    say("wide batch", case, "V", V, "k", k, "rows", rows, S.path)
     if pen:
         S.sample_batch(dev(torch, x), dev(torch, u), out, dev(torch, off), dev(torch, ids))
     else:
@@ -119,8 +127,26 @@ def test_wide_batch(torch_cuda, K, oracle_lib, case):
     got = out.cpu().numpy()
     for r in range(rows):
         counts = W.counts_of(hists[r], V) if pen else None
-        t = check_row(S, O, x[r], p, u[r], counts, r, f"case{case}")
-        assert got[r] == t, (case, r, got[r], t)
+        t = check_row(S, O, x[r], p, u[r], counts, r, label)
+        assert got[r] == t, (label, r, got[r], t)
+
+
+@pytest.mark.parametrize("pen", [0, 1])
+def test_wide_tile_size_changes(torch_cuda, K, oracle_lib, pen):
+    """One handle whose calls change the sort's tile size: 64 rows of 30,001 ids sort in tiles of 8,192 keys, 32
+    rows in tiles of 4,096, one row in tiles of 2,048, then 64 rows again. Each call writes the first radix
+    digit's counts afresh for every tile (the keys kernel, or the sort's histogram kernel), so nothing of an
+    earlier call's counts may reach a later one."""
+    torch = torch_cuda
+    O = oracle_lib
+    V = 30001
+    rng = np.random.default_rng(950 + pen)
+    p = W.Params(temperature=0.9, top_k=0, top_p=0.93, **PENS[pen])
+    S = K.Sampler(p, n_vocab=V, max_rows=64)
+    assert S.path == "wide"
+    for step, rows in enumerate((64, 32, 1, 64)):
+        say("wide tile size changes", "pen", pen, "step", step, "rows", rows)
+        run_batch(torch, S, O, rng, head_rows(rng, rows, V), p, pen, 400 if pen else 0, f"pen{pen} step{step}")
     S.close()
 
 
