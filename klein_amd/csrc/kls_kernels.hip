@@ -2108,6 +2108,8 @@ __shared__ WideSeg s_wt_flat[WT_FLAT];
 __shared__ double s_wt_acc;                               // the resolve walk's state, handed between waves
 __shared__ int s_wt_i, s_wt_st, s_wt_rs, s_wt_re;
 __shared__ int s_wt_off[TAIL_WG + 1];
+__shared__ uint16_t s_wt_rc[WT_FLAT];  // the window's chunk (from cb) of each record
+static_assert(TAIL_WG <= 65536, "a window's chunk index fits 16 bits");
 __shared__ int s_wt_wsum[TAIL_WG / 64];
 
 // Composition for a segmented scan: bit 2 of p marks a map that starts a segment (nothing before it applies).
@@ -2423,14 +2425,14 @@ __device__ double wt_resolve(const RowsArgs& a, const WideArgs& w, int row, cons
         if (tid == 0) s_wt_off[0] = 0;
         const int fit = __syncthreads_count(cb + tid < nc && cs <= WT_FLAT);
         const int ce = cb + max(fit, 1), wn = s_wt_off[ce - cb];
+        // each chunk of the window marks its records with its index (s_wt_off[tid + 1] <= wn <= WT_FLAT), so that
+        // a record finds its chunk with one LDS read instead of a binary search over the offsets
+        if (tid < ce - cb)
+            for (int r = s_wt_off[tid]; r < s_wt_off[tid + 1]; ++r) s_wt_rc[r] = (uint16_t) tid;
+        __syncthreads();
         for (int r = tid; r < wn; r += TAIL_WG) {
-            int lo_c = 0, hi_c = ce - cb - 1;  // the chunk of record r: the last cc with s_wt_off[cc] <= r
-            while (lo_c < hi_c) {
-                const int mid = (lo_c + hi_c + 1) >> 1;
-                if (s_wt_off[mid] <= r) lo_c = mid;
-                else hi_c = mid - 1;
-            }
-            s_wt_flat[r] = seg[(int64_t) (cb + lo_c) * WT_SEGS + (r - s_wt_off[lo_c])];
+            const int c = s_wt_rc[r];
+            s_wt_flat[r] = seg[(int64_t) (cb + c) * WT_SEGS + (r - s_wt_off[c])];
         }
         __syncthreads();
         cb = ce;
