@@ -55,7 +55,7 @@ typedef void* kls_stream;
  * max_rows bounds the rows of kls_verify and kls_sample_batch. A top-k of 65 to 1024 takes the mid path: one
  * kernel, like top-k <= 64, with a 128 KB candidate buffer per row (vocabularies of up to 16384 / top_k segments
  * of 32768 ids: n_vocab <= 524,288 for every such top-k). A larger top-k (or no limit) takes a slower path
- * that keys and sorts every logit of a row (2 x 8 bytes per logit per row of device memory, plus ~3.6 KB per
+ * that keys and sorts every logit of a row (2 x 8 bytes per logit per row of device memory, plus ~6.2 KB per
  * 2,048 ids per row for the sort's digit counts and the tail's chunk records; a key kernel, a radix sort's passes and the tail's kernels,
  * captured together in a verify step's graph); it needs n_vocab * max_rows below 2^32 (KLS_ERR_UNSUPPORTED
  * otherwise). */
