@@ -50,7 +50,10 @@ __device__ __forceinline__ int tile_offset(int wave, int s, int lane) { return w
 template <int PER>
 __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __restrict__ in, uint32_t row_len,
                                                           uint32_t tpr, int shift, uint32_t* __restrict__ counts) {
-    __shared__ uint32_t h[256];
+    // four sub-tables, picked by lane & 3 and padded apart, so that a wave's lanes with one digit (most keys share
+    // a few digits in the sign and exponent passes) add to four addresses in four banks, not one
+    constexpr int HC = 4, HP = 257;
+    __shared__ uint32_t h[HC * HP];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t row = blockIdx.x / tpr, t = blockIdx.x - row * tpr;
     constexpr int TILE = PER * ST_WG;
@@ -62,13 +65,14 @@ __global__ __launch_bounds__(ST_WG) void sort_hist_kernel(const uint64_t* __rest
         const int i = tile_offset<PER>(wave, s, lane);
         k[s] = i < lim ? src[i] : 0ull;
     }
-    if (tid < 256) h[tid] = 0u;
+    for (int i = tid; i < HC * HP; i += ST_WG) h[i] = 0u;
     __syncthreads();
+    uint32_t* const hl = h + (lane & (HC - 1)) * HP;
 #pragma unroll
     for (int s = 0; s < PER; ++s)
-        if (tile_offset<PER>(wave, s, lane) < lim) atomicAdd(&h[rdigit(k[s], shift)], 1u);
+        if (tile_offset<PER>(wave, s, lane) < lim) atomicAdd(&hl[rdigit(k[s], shift)], 1u);
     __syncthreads();
-    if (tid < 256) counts[(size_t) blockIdx.x * 256 + tid] = h[tid];
+    if (tid < 256) counts[(size_t) blockIdx.x * 256 + tid] = h[tid] + h[HP + tid] + h[2 * HP + tid] + h[3 * HP + tid];
 }
 
 constexpr int SC_UNROLL = 16;  // count-table rows in flight per thread
