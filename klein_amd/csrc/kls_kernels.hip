@@ -1595,10 +1595,11 @@ __shared__ int s_wide_n;  // kk, then the min-p length
 // integer in [2^52, 2^53), and RN(A*u + t) = (A + d)*u where, writing t/u = f + phi (f integer, 0 <= phi < 1),
 // d = f when phi < 1/2, f + 1 when phi > 1/2, and at a tie (phi = 1/2) whichever of f, f + 1 makes A + d even.
 // So each term is a map of the parity of A: (d for parity 0, d for parity 1, parity after each). Maps compose
-// associatively, so a workgroup scans 8,192 terms at a time (8 per thread) and knows every A on the way. A term
+// associatively, so a workgroup scans a block of terms at a time (replay_sum: TAIL_WG threads, one or two terms
+// each; the wide tail's map kernels: a chunk of WT_CHUNK) and knows every A on the way. A term
 // whose exact sum could leave the binade (A + f < 2^52, or A + f >= 2^53 - 1, or t/u huge) is added with the real
 // double addition instead, and the scan restarts after it in the new binade; so is every term while acc is 0 or
-// subnormal. Identical results to the sequential loop, in ~31 workgroup steps for 248,320 terms.
+// subnormal. Identical results to the sequential loop, in one workgroup step per block and per binade change.
 // Increments are integers held in doubles: while no term leaves the binade every increment and every partial
 // count is below 2^53 in magnitude, so the double arithmetic on them is exact (and full rate, with no integer
 // conversions); past a term that leaves the binade the values are discarded anyway.
